@@ -1,0 +1,217 @@
+#!/usr/bin/env python3
+"""Benchmark of the bs=1 Q4_K_M Llama decode path on one MI355X.
+
+Workload (the configuration the headline metric is quoted on): a Llama-3 8B-shape random-init
+GGUF quantized Q4_K_M (token_embd/output Q6_K, other matrices Q4_K, norms F32), generated from
+a fixed seed; end-to-end through the LlmEngine mirror at batch 1 with run_benchmark's greedy
+parameters (temperature 0, top_p 1, repeat_penalty 1): a 2048-token seeded random prompt, then
+greedy decode.  A "step" is one decode token.  --warmup W decode tokens run in an untimed first
+infer; the timed infer decodes --steps K tokens.  value = K / decode seconds, the reference's
+tokens_per_sec = tokens_generated / decode_s with decode timed from the first token to the end
+(run_benchmark, src-tauri/src/commands.rs:542-564).  Weights and KV are resident in HBM before
+the timed region.
+
+roofline: the Q4_K fused dequant-GEMV at 4096 -> 14336 (the gate/up shape), timed with HIP
+events on the context's stream over back-to-back launches that rotate through distinct weight
+copies (> 1 GB, more than the 256 MB Infinity Cache).  Algorithmic bytes per launch =
+K*N*144/256 + 4K + 4N.  traffic comes from the committed rocprofv3 PMC summary when present.
+
+cpu_baseline: the CPU oracle's restatement of candle's CPU decode (Q8_K activation quant,
+integer vec_dot, OpenMP over output columns) timed on this host's cores on a bounded sample of
+the same model: a short prompt, then greedy decode steps for about 20 s.
+"""
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "tpt-spark_amd"))
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "decode tok/s (bs=1, 8B-shape Q4_K_M) + Q4_K GEMV achieved HBM GB/s vs peak"
+PROMPT_LEN = 2048
+SEED = 20261201
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gemv_roofline(tp, ctx, iters=256):
+    """Event-timed Q4_K GEMV at the config-2 shapes, rotating through >= 1 GB of copies."""
+    from tpthip import synth
+    out = {}
+    for K, N in [(4096, 14336), (14336, 4096), (4096, 4096), (4096, 1024)]:
+        w = synth.random_weights(tp.TYPE_Q4_K, N, K, seed=K + N, name=f"bench{K}x{N}")
+        n_copies = max(2, int(np.ceil(1.1e9 / w.nbytes)))
+        bufs = [ctx.to_device(w) for _ in range(n_copies)]
+        x = ctx.to_device(np.random.default_rng(1).standard_normal(K).astype(np.float32))
+        y = ctx.alloc(N * 4)
+        ctx.bench_gemv(tp.TYPE_Q4_K, bufs, x, y, K, N, n_copies)  # warm-up pass
+        ms = ctx.bench_gemv(tp.TYPE_Q4_K, bufs, x, y, K, N, iters)
+        alg = K * N * 144 // 256 + 4 * K + 4 * N
+        us = ms * 1e3 / iters
+        out[f"{K}x{N}"] = {"bytes": alg, "us_per_launch": round(us, 3),
+                           "gbs": round(alg / (us * 1e-6) / 1e9, 1), "copies": n_copies}
+        log(f"gemv q4_k {K}->{N}: {us:.2f} us/launch, {alg / (us * 1e-6) / 1e9:.0f} GB/s")
+        for b in bufs:
+            b.free()
+    return out
+
+
+def cpu_baseline(path, budget_s=20.0):
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    threads = min(os.cpu_count() or 1, 16)
+    m = oracle.Model(path)
+    m.reset(64)
+    rng = np.random.default_rng(SEED)
+    prompt = rng.integers(0, m.cfg["vocab"], 4).tolist()
+    logits = m.forward(prompt, 0, threads)
+    tok = oracle.argmax(logits)
+    pos, n, t0 = len(prompt), 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s and pos < 64:
+        tok = oracle.argmax(m.forward([tok], pos, threads))
+        pos += 1
+        n += 1
+    dt = time.perf_counter() - t0
+    m.close()
+    return {"value": round(n / dt, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"8B-shape Q4_K_M, 4-token prompt then {n} greedy decode steps "
+                      f"({dt:.1f} s) on {threads} host threads"}
+
+
+def traffic_from_profiles(key):
+    p = os.path.join(ROOT, "profiles", "gemv_q4k_traffic.json")
+    if not os.path.exists(p):
+        return None
+    try:
+        return json.load(open(p)).get(key, {}).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256, help="timed decode tokens")
+    ap.add_argument("--warmup", type=int, default=16, help="untimed decode tokens")
+    ap.add_argument("--prompt", type=int, default=PROMPT_LEN)
+    ap.add_argument("--model", default="", help="existing GGUF (default: generate the 8B shape)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--leg", choices=["all", "gemv"], default="all",
+                    help="gemv: only the GEMV roofline leg (for PMC profiling)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the path runs on a single MI355X; see DESIGN.md for how it would shard)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import tpthip as tp
+    from tpthip import synth
+
+    ctx = tp.Context(0)
+    log(f"device: {ctx.name}, {ctx.n_cu} CUs")
+    gemv = gemv_roofline(tp, ctx)
+    if args.leg == "gemv":
+        print(json.dumps({"gemv": gemv}))
+        return
+
+    tmpdir = tempfile.mkdtemp(prefix="tpt_bench_", dir=os.environ.get("TPT_BENCH_DIR") or None)
+    path = args.model
+    if not path:
+        path = os.path.join(tmpdir, "llama3-8b-shape-q4_k_m.gguf")
+        t0 = time.perf_counter()
+        synth.write_llama(path, synth.LLAMA_8B, seed=SEED, nthreads=min(os.cpu_count() or 1, 16))
+        log(f"generated {path} ({os.path.getsize(path) / 1e9:.2f} GB) in {time.perf_counter() - t0:.1f} s")
+    try:
+        eng = tp.HipEngine(0)
+        t0 = time.perf_counter()
+        info = eng.load(path)
+        log(f"loaded {info.name} ({info.size_bytes / 1e9:.2f} GB) backend={info.backend} in "
+            f"{time.perf_counter() - t0:.1f} s")
+        m = eng  # noqa: F841
+        desc_model = tp.Model  # noqa: F841
+        rng = np.random.default_rng(SEED)
+        prompt = rng.integers(0, 128256, args.prompt).tolist()
+        # warm-up infer (graph capture, first-touch), then a cold cache for the timed run
+        eng.infer(tp.greedy_params(prompt, args.warmup), lambda ev: None)
+        eng.reset_cache()
+        n_tok = [0]
+
+        def on_tok(ev):
+            if not ev.done:
+                n_tok[0] += 1
+
+        st = eng.infer(tp.greedy_params(prompt, args.steps), on_tok)
+        assert st.generated == args.steps == n_tok[0], (st.generated, n_tok[0])
+        decode_s = st.decode_ms / 1e3
+        tok_s = args.steps / decode_s
+        prefill_tok_s = len(prompt) / (st.ttft_ms / 1e3)
+        # decode ceiling from the model's streamed bytes per token
+        probe = tp.Model(ctx, path, max_ctx=64)
+        bpt = probe.desc["decode_bytes_per_token"]
+        probe.close()
+        ceiling = HBM_PEAK_GBS * 1e9 / bpt
+        kv_bpt = 32 * 2 * 8 * 128 * 2 * (len(prompt) + args.steps / 2)
+        log(f"prefill {len(prompt)} tok in {st.ttft_ms:.0f} ms ({prefill_tok_s:.1f} tok/s); decode "
+            f"{args.steps} tok in {st.decode_ms:.1f} ms = {tok_s:.1f} tok/s; ceiling {ceiling:.1f}")
+        eng.close()
+        cpu = None if args.no_cpu else cpu_baseline(path)
+    finally:
+        if not args.model and os.path.exists(path):
+            os.remove(path)
+        try:
+            os.rmdir(tmpdir)
+        except OSError:
+            pass
+
+    g = gemv["4096x14336"]
+    line = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(st.decode_ms / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": "llama-3-8b-shape random-init GGUF Q4_K_M (token_embd/output Q6_K, "
+                        "matrices Q4_K), bs=1, 2048-token seeded prompt then greedy decode "
+                        "through the LlmEngine mirror",
+            "prompt_tokens": len(prompt),
+            "prefill_tok_s": round(prefill_tok_s, 2),
+            "weight_bytes_per_token": bpt,
+            "decode_ceiling_tok_s": round(ceiling, 1),
+            "decode_frac_of_ceiling": round(tok_s / ceiling, 4),
+            "decode_frac_of_ceiling_with_kv": round(tok_s / (HBM_PEAK_GBS * 1e9 / (bpt + kv_bpt)), 4),
+            "arith": "q4_k/q6_k weights x q8_k activations: int8 dot4 -> int32, f32 block scales",
+            "gemv_q4k": gemv,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "gemv_q8_kernel<Q4_K> 4096->14336",
+            "achieved": g["gbs"],
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(g["gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": traffic_from_profiles("4096x14336"),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,276 @@
+// C ABI: error reporting, context, device memory and the op-level entry points.
+#include <stdio.h>
+
+#include <cmath>
+#include <string>
+
+#include "kernels.h"
+
+namespace tpt {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what, const char* file, int line) {
+  char buf[512];
+  snprintf(buf, sizeof buf, "HIP error %d (%s) in %s at %s:%d", (int)e, hipGetErrorString(e), what,
+           file, line);
+  g_last_error = buf;
+  return e == hipErrorOutOfMemory ? TPT_ERR_OOM : TPT_ERR_HIP;
+}
+
+int ctx_enter(tpt_ctx* c) {
+  if (!c) return fail(TPT_ERR_INVALID, "null context");
+  TPT_HIP(hipSetDevice(c->device));
+  return TPT_OK;
+}
+
+}  // namespace tpt
+
+using namespace tpt;
+
+#define ENTER(c)                        \
+  do {                                  \
+    int _rc = ::tpt::ctx_enter(c);      \
+    if (_rc) return _rc;                \
+  } while (0)
+
+extern "C" {
+
+const char* tpt_last_error(void) { return g_last_error.c_str(); }
+int tpt_version(void) { return 1; }
+
+int tpt_ctx_create(int device, tpt_ctx** out) {
+  if (!out) return fail(TPT_ERR_INVALID, "null out pointer");
+  int n = 0;
+  TPT_HIP(hipGetDeviceCount(&n));
+  if (device < 0 || device >= n) return fail(TPT_ERR_INVALID, "device index out of range");
+  TPT_HIP(hipSetDevice(device));
+  tpt_ctx* c = new tpt_ctx();
+  c->device = device;
+  hipDeviceProp_t prop;
+  hipError_t e = hipGetDeviceProperties(&prop, device);
+  if (e == hipSuccess) {
+    c->n_cu = prop.multiProcessorCount;
+    snprintf(c->name, sizeof c->name, "%s (%s)", prop.name, prop.gcnArchName);
+  }
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete c;
+    return hip_fail(e, "tpt_ctx_create", __FILE__, __LINE__);
+  }
+  *out = c;
+  return TPT_OK;
+}
+
+int tpt_ctx_destroy(tpt_ctx* c) {
+  if (!c) return TPT_OK;
+  ENTER(c);
+  (void)hipStreamSynchronize(c->stream);
+  (void)hipStreamDestroy(c->stream);
+  delete c;
+  return TPT_OK;
+}
+
+int tpt_ctx_synchronize(tpt_ctx* c) {
+  ENTER(c);
+  TPT_HIP(hipStreamSynchronize(c->stream));
+  return TPT_OK;
+}
+
+int tpt_ctx_device_info(tpt_ctx* c, int* n_cu, char* name, int name_len) {
+  ENTER(c);
+  if (n_cu) *n_cu = c->n_cu;
+  if (name && name_len > 0) snprintf(name, (size_t)name_len, "%s", c->name);
+  return TPT_OK;
+}
+
+int tpt_malloc(tpt_ctx* c, size_t bytes, void** dptr) {
+  ENTER(c);
+  if (!dptr) return fail(TPT_ERR_INVALID, "null out pointer");
+  TPT_HIP(hipMalloc(dptr, bytes ? bytes : 1));
+  return TPT_OK;
+}
+
+int tpt_free(tpt_ctx* c, void* dptr) {
+  ENTER(c);
+  if (dptr) TPT_HIP(hipFree(dptr));
+  return TPT_OK;
+}
+
+int tpt_memcpy_h2d(tpt_ctx* c, void* dst, const void* src, size_t bytes) {
+  ENTER(c);
+  TPT_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream));
+  TPT_HIP(hipStreamSynchronize(c->stream));
+  return TPT_OK;
+}
+
+int tpt_memcpy_d2h(tpt_ctx* c, void* dst, const void* src, size_t bytes) {
+  ENTER(c);
+  TPT_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream));
+  TPT_HIP(hipStreamSynchronize(c->stream));
+  return TPT_OK;
+}
+
+int tpt_memset(tpt_ctx* c, void* dst, int value, size_t bytes) {
+  ENTER(c);
+  TPT_HIP(hipMemsetAsync(dst, value, bytes, c->stream));
+  return TPT_OK;
+}
+
+int tpt_dequant(tpt_ctx* c, int type, const void* w, float* y, int64_t n) {
+  ENTER(c);
+  if (!w || !y) return fail(TPT_ERR_INVALID, "dequant: null pointer");
+  return launch_dequant(type, w, y, n, c->stream);
+}
+
+int tpt_gemv(tpt_ctx* c, int type, const void* w, const float* x, float* y, int K, int N,
+             int act_mode) {
+  ENTER(c);
+  if (!w || !x || !y) return fail(TPT_ERR_INVALID, "gemv: null pointer");
+  if (act_mode == TPT_ACT_F32) return launch_gemv_f32(type, (const uint8_t*)w, x, y, K, N, c->stream);
+  if (act_mode != TPT_ACT_Q8) return fail(TPT_ERR_INVALID, "gemv: act_mode must be TPT_ACT_Q8 or TPT_ACT_F32");
+  GemvArgs a;
+  a.w0 = (const uint8_t*)w;
+  a.row_stride = row_bytes(type, K);
+  a.K = K;
+  a.N = N;
+  a.x = x;
+  a.y = y;
+  return launch_gemv_q8(c, type, a, c->stream);
+}
+
+int tpt_gemv_rmsnorm(tpt_ctx* c, int type, const void* w, const float* x, const float* norm_w,
+                     float eps, float* y, int K, int N) {
+  ENTER(c);
+  if (!w || !x || !y || !norm_w) return fail(TPT_ERR_INVALID, "gemv_rmsnorm: null pointer");
+  GemvArgs a;
+  a.w0 = (const uint8_t*)w;
+  a.row_stride = row_bytes(type, K);
+  a.K = K;
+  a.N = N;
+  a.x = x;
+  a.norm_w = norm_w;
+  a.eps = eps;
+  a.prologue = PRO_RMSNORM;
+  a.y = y;
+  return launch_gemv_q8(c, type, a, c->stream);
+}
+
+int tpt_rmsnorm(tpt_ctx* c, const float* x, const float* w, float* y, int n, float eps) {
+  ENTER(c);
+  if (!x || !w || !y) return fail(TPT_ERR_INVALID, "rmsnorm: null pointer");
+  return launch_rmsnorm(x, w, y, n, eps, c->stream);
+}
+
+int tpt_rope(tpt_ctx* c, float* x, int n_heads, int hd, int pos, const float* cos_t,
+             const float* sin_t) {
+  ENTER(c);
+  if (!x || !cos_t || !sin_t) return fail(TPT_ERR_INVALID, "rope: null pointer");
+  return launch_rope(x, n_heads, hd, pos, cos_t, sin_t, c->stream);
+}
+
+int tpt_attn_decode(tpt_ctx* c, const float* q, const void* k_cache, const void* v_cache,
+                    float* o, int nq, int nkv, int hd, int L, int L_stride, int n_chunks) {
+  ENTER(c);
+  if (!q || !k_cache || !v_cache || !o) return fail(TPT_ERR_INVALID, "attention: null pointer");
+  if (nkv <= 0 || nq <= 0 || nq % nkv) return fail(TPT_ERR_INVALID, "attention: bad head counts");
+  AttnArgs a;
+  a.q = q;
+  a.kc = (const uint16_t*)k_cache;
+  a.vc = (const uint16_t*)v_cache;
+  a.o = o;
+  a.nq = nq;
+  a.nkv = nkv;
+  a.hd = hd;
+  a.L_stride = L_stride;
+  a.L_host = L;
+  a.n_chunks = n_chunks > 0 ? n_chunks : attn_default_chunks(L, nkv);
+  // per-call scratch: partial records and the per-kv-head arrival counters
+  const size_t pf = (size_t)attn_part_floats(nq, nkv, hd, a.n_chunks);
+  void* scratch = nullptr;
+  TPT_HIP(hipMallocAsync(&scratch, pf * 4 + 256 + (size_t)nkv * 4, c->stream));
+  a.part = (float*)scratch;
+  a.counters = (unsigned int*)((char*)scratch + ((pf * 4 + 255) & ~(size_t)255));
+  hipError_t e = hipMemsetAsync(a.counters, 0, (size_t)nkv * 4, c->stream);
+  int rc = e == hipSuccess ? launch_attn_decode(a, c->stream) : hip_fail(e, "memset", __FILE__, __LINE__);
+  (void)hipFreeAsync(scratch, c->stream);
+  return rc;
+}
+
+int tpt_argmax(tpt_ctx* c, const float* logits, int64_t n, uint32_t* out_host) {
+  ENTER(c);
+  if (!logits || !out_host) return fail(TPT_ERR_INVALID, "argmax: null pointer");
+  unsigned long long* slot = nullptr;
+  TPT_HIP(hipMallocAsync((void**)&slot, 8, c->stream));
+  hipError_t e = hipMemsetAsync(slot, 0, 8, c->stream);
+  int rc = e == hipSuccess ? launch_argmax(logits, n, slot, c->stream) : hip_fail(e, "memset", __FILE__, __LINE__);
+  unsigned long long key = 0;
+  if (rc == TPT_OK) {
+    e = hipMemcpyAsync(&key, slot, 8, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) rc = hip_fail(e, "argmax readback", __FILE__, __LINE__);
+  }
+  (void)hipFreeAsync(slot, c->stream);
+  if (rc == TPT_OK) *out_host = (uint32_t)(key & 0xffffffffull);
+  return rc;
+}
+
+int tpt_bench_gemv(tpt_ctx* c, int type, const void* const* weights, int n_weights,
+                   const float* x, float* y, int K, int N, int iters, float* ms_out) {
+  ENTER(c);
+  if (!weights || n_weights <= 0 || iters <= 0 || !x || !y || !ms_out)
+    return fail(TPT_ERR_INVALID, "bench_gemv: bad arguments");
+  GemvArgs a;
+  a.row_stride = row_bytes(type, K);
+  a.K = K;
+  a.N = N;
+  a.x = x;
+  a.y = y;
+  hipEvent_t e0, e1;
+  TPT_HIP(hipEventCreate(&e0));
+  TPT_HIP(hipEventCreate(&e1));
+  int rc = TPT_OK;
+  hipError_t e = hipEventRecord(e0, c->stream);
+  for (int i = 0; i < iters && rc == TPT_OK && e == hipSuccess; i++) {
+    a.w0 = (const uint8_t*)weights[i % n_weights];
+    rc = launch_gemv_q8(c, type, a, c->stream);
+  }
+  if (e == hipSuccess) e = hipEventRecord(e1, c->stream);
+  if (e == hipSuccess) e = hipEventSynchronize(e1);
+  if (e == hipSuccess && rc == TPT_OK) e = hipEventElapsedTime(ms_out, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (rc) return rc;
+  if (e != hipSuccess) return hip_fail(e, "bench_gemv", __FILE__, __LINE__);
+  return TPT_OK;
+}
+
+int tpt_bench_copy(tpt_ctx* c, void* dst, const void* src, size_t bytes, int iters,
+                   float* ms_out) {
+  ENTER(c);
+  if (!dst || !src || iters <= 0 || !ms_out || bytes % 16) return fail(TPT_ERR_INVALID, "bench_copy: bad arguments");
+  hipEvent_t e0, e1;
+  TPT_HIP(hipEventCreate(&e0));
+  TPT_HIP(hipEventCreate(&e1));
+  int rc = TPT_OK;
+  hipError_t e = hipEventRecord(e0, c->stream);
+  for (int i = 0; i < iters && rc == TPT_OK && e == hipSuccess; i++)
+    rc = launch_copy(dst, src, bytes, c->stream);
+  if (e == hipSuccess) e = hipEventRecord(e1, c->stream);
+  if (e == hipSuccess) e = hipEventSynchronize(e1);
+  if (e == hipSuccess && rc == TPT_OK) e = hipEventElapsedTime(ms_out, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (rc) return rc;
+  if (e != hipSuccess) return hip_fail(e, "bench_copy", __FILE__, __LINE__);
+  return TPT_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,201 @@
+// Small kernels of the decode path: bit-exact dequantization, the decode-step prologue
+// (token pick + embedding row), RMSNorm, RoPE and argmax as standalone ops.
+#include "kernels.h"
+
+namespace tpt {
+namespace {
+
+// One element of a GGUF row, dequantized with candle's to_float arithmetic (bit-exact):
+//   Q4_K: (d*sc)*q - dmin*m     (candle BlockQ4K::to_float; ggml dequantize_row_q4_K order)
+//   Q6_K: (d*sc)*(q-32)         (candle BlockQ6K::to_float; dequant_q6k.wgsl:9-24 layout)
+//   Q8_0: d*q                   (candle BlockQ8_0::to_float; dequant_q8.wgsl:3-6)
+__device__ __forceinline__ float dequant_elem(int type, const uint8_t* base, int64_t i) {
+  if (type == TPT_TYPE_Q4_K) {
+    const uint8_t* b = base + (i >> 8) * 144;
+    const int j = (int)(i & 255), g = j >> 6, l = j & 63;
+    const int sub = 2 * g + (l >= 32);
+    const uint8_t qb = b[16 + 32 * g + (l & 31)];
+    const int q = l < 32 ? (qb & 0xF) : (qb >> 4);
+    const uint8_t* s = b + 4;
+    int sc, m;
+    if (sub < 4) {
+      sc = s[sub] & 63;
+      m = s[sub + 4] & 63;
+    } else {
+      sc = (s[sub + 4] & 0xF) | ((s[sub - 4] >> 6) << 4);
+      m = (s[sub + 4] >> 4) | ((s[sub] >> 6) << 4);
+    }
+    const float d = h2f(ldg_u<uint16_t>(b)), dmin = h2f(ldg_u<uint16_t>(b + 2));
+    const float d1 = d * (float)sc, m1 = dmin * (float)m;
+    return d1 * (float)q - m1;
+  }
+  if (type == TPT_TYPE_Q6_K) {
+    const uint8_t* b = base + (i >> 8) * 210;
+    const int j = (int)(i & 255), p = j >> 7, r = j & 127, quad = r >> 5, l = r & 31;
+    const uint8_t qlb = b[64 * p + 32 * (quad & 1) + l];
+    const int lo = quad >= 2 ? (qlb >> 4) : (qlb & 0xF);
+    const int hi = (b[128 + 32 * p + l] >> (2 * quad)) & 3;
+    const int q = (lo | (hi << 4)) - 32;
+    const int sc = (int8_t)b[192 + 8 * p + (l >> 4) + 2 * quad];
+    const float d = h2f(ldg_u<uint16_t>(b + 208));
+    return d * (float)sc * (float)q;
+  }
+  if (type == TPT_TYPE_Q8_0) {
+    const uint8_t* b = base + (i >> 5) * 34;
+    return h2f(ldg_u<uint16_t>(b)) * (float)(int8_t)b[2 + (i & 31)];
+  }
+  if (type == TPT_TYPE_F16) return h2f(ldg_u<uint16_t>(base + 2 * i));
+  return ldg_u<float>(base + 4 * i);
+}
+
+__global__ void dequant_kernel(int type, const uint8_t* __restrict__ w, float* __restrict__ y,
+                               int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    y[i] = dequant_elem(type, w, i);
+}
+
+__global__ void __launch_bounds__(256) step_begin_kernel(StepState* st, const uint32_t* prompt,
+                                                         int embd_type, const uint8_t* embd,
+                                                         size_t embd_row_bytes, int H, int vocab,
+                                                         float* x, uint32_t* tok_log) {
+  __shared__ uint32_t s_tok;
+  __shared__ int s_pos;
+  if (threadIdx.x == 0) {
+    const int pos = st->next_pos;
+    uint32_t tok;
+    if (pos < st->prompt_len) tok = prompt[pos];
+    else if (st->use_override) tok = st->tok_override;
+    else tok = (uint32_t)(st->amax[st->parity] & 0xffffffffull);
+    if (tok >= (uint32_t)vocab) tok = (uint32_t)(vocab - 1);  // never index past the table
+    s_tok = tok;
+    s_pos = pos;
+  }
+  __syncthreads();
+  const uint8_t* row = embd + (size_t)s_tok * embd_row_bytes;
+  for (int i = threadIdx.x; i < H; i += blockDim.x) x[i] = dequant_elem(embd_type, row, i);
+  if (threadIdx.x == 0) {
+    const int np = st->parity ^ 1;
+    st->pos = s_pos;
+    st->next_pos = s_pos + 1;
+    st->parity = np;
+    st->amax[np] = 0ull;
+    st->use_override = 0;
+    if (tok_log) tok_log[s_pos] = s_tok;
+  }
+}
+
+// candle_nn::ops::rms_norm: m = sqrt(sum(x^2)/n + eps); y = x / m * w (one workgroup)
+__global__ void __launch_bounds__(1024) rmsnorm_kernel(const float* __restrict__ x,
+                                                       const float* __restrict__ w,
+                                                       float* __restrict__ y, int n, float eps) {
+  __shared__ float red[16];
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) ss = fmaf(x[i], x[i], ss);
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < (int)(blockDim.x >> 6); i++) t += red[i];
+  const float m = sqrtf(t / (float)n + eps);
+  for (int i = threadIdx.x; i < n; i += blockDim.x) y[i] = x[i] / m * w[i];
+}
+
+// candle rope_i over n_heads heads of hd at one position
+__global__ void rope_kernel(float* __restrict__ x, int n_pairs, int hd, int pos,
+                            const float* __restrict__ c, const float* __restrict__ s) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n_pairs) return;
+  const int i = t % (hd / 2);
+  const float cs = c[(size_t)pos * (hd / 2) + i], sn = s[(size_t)pos * (hd / 2) + i];
+  const float x0 = x[2 * t], x1 = x[2 * t + 1];
+  x[2 * t] = x0 * cs - x1 * sn;
+  x[2 * t + 1] = x0 * sn + x1 * cs;
+}
+
+__global__ void __launch_bounds__(256) argmax_kernel(const float* __restrict__ v, int64_t n,
+                                                     unsigned long long* slot) {
+  unsigned long long best = 0;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const unsigned long long k = ((unsigned long long)order_key(v[i]) << 32) | (unsigned long long)i;
+    best = k > best ? k : best;
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const unsigned long long ob = __shfl_xor(best, o, WAVE);
+    best = ob > best ? ob : best;
+  }
+  if ((threadIdx.x & 63) == 0) atomicMax(slot, best);
+}
+
+// plain 16-byte vector copy, grid-stride (HBM calibration reference)
+__global__ void __launch_bounds__(256) copy_kernel(uint4* __restrict__ dst,
+                                                   const uint4* __restrict__ src, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
+
+}  // namespace
+
+int launch_copy(void* dst, const void* src, size_t bytes, hipStream_t s) {
+  const size_t n = bytes / 16;
+  size_t blocks = (n + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  if (blocks == 0) return TPT_OK;
+  hipLaunchKernelGGL(copy_kernel, dim3((unsigned)blocks), dim3(256), 0, s, (uint4*)dst,
+                     (const uint4*)src, n);
+  TPT_HIP(hipGetLastError());
+  return TPT_OK;
+}
+
+int launch_dequant(int type, const void* w, float* y, int64_t n, hipStream_t s) {
+  const int bs = type_block(type);
+  if (type_bytes(type) == 0) return fail(TPT_ERR_UNSUPPORTED, "dequant: unsupported type");
+  if (n < 0 || n % bs) return fail(TPT_ERR_INVALID, "dequant: n must be a multiple of the block size");
+  if (n == 0) return TPT_OK;
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)blocks), dim3(256), 0, s, type,
+                     (const uint8_t*)w, y, n);
+  TPT_HIP(hipGetLastError());
+  return TPT_OK;
+}
+
+int launch_step_begin(StepState* st, const uint32_t* prompt, int embd_type, const uint8_t* embd,
+                      size_t embd_row_bytes, int H, int vocab, float* x, uint32_t* tok_log,
+                      hipStream_t s) {
+  hipLaunchKernelGGL(step_begin_kernel, dim3(1), dim3(256), 0, s, st, prompt, embd_type, embd,
+                     embd_row_bytes, H, vocab, x, tok_log);
+  TPT_HIP(hipGetLastError());
+  return TPT_OK;
+}
+
+int launch_rmsnorm(const float* x, const float* w, float* y, int n, float eps, hipStream_t s) {
+  if (n <= 0) return fail(TPT_ERR_INVALID, "rmsnorm: n must be positive");
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(1024), 0, s, x, w, y, n, eps);
+  TPT_HIP(hipGetLastError());
+  return TPT_OK;
+}
+
+int launch_rope(float* x, int n_heads, int hd, int pos, const float* c, const float* sn,
+                hipStream_t s) {
+  if (n_heads <= 0 || hd <= 0 || (hd & 1) || pos < 0) return fail(TPT_ERR_INVALID, "rope: bad shape");
+  const int pairs = n_heads * hd / 2;
+  hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, s, x, pairs,
+                     hd, pos, c, sn);
+  TPT_HIP(hipGetLastError());
+  return TPT_OK;
+}
+
+int launch_argmax(const float* logits, int64_t n, unsigned long long* slot, hipStream_t s) {
+  if (n <= 0 || n > 0xffffffffll) return fail(TPT_ERR_INVALID, "argmax: bad length");
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 1024) blocks = 1024;
+  hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)blocks), dim3(256), 0, s, logits, n, slot);
+  TPT_HIP(hipGetLastError());
+  return TPT_OK;
+}
+
+}  // namespace tpt

@@ -1,0 +1,86 @@
+// Kernel launch interfaces shared by the C ABI, the model and the tests' entry points.
+#pragma once
+#include "tpt_common.h"
+
+namespace tpt {
+
+enum GemvPrologue { PRO_PLAIN = 0, PRO_RMSNORM = 1 };
+enum GemvEpilogue {
+  EPI_STORE = 0,     // y[r] = acc
+  EPI_RESID = 1,     // y[r] = acc + resid[r]   (resid may alias y)
+  EPI_ROPE_QKV = 2,  // rows [0,qd) -> q (RoPE), [qd,qd+kd) -> k cache (RoPE, fp16), rest -> v cache
+  EPI_SWIGLU = 3,    // two matrices: y[r] = silu(acc0) * acc1
+  EPI_ARGMAX = 4,    // y[r] = acc (if y) + device argmax into amax slot
+};
+
+// Decode-step state kept in device memory so one captured graph serves every step.
+struct StepState {
+  int pos;             // position processed by the current step
+  int next_pos;        // position of the next step
+  int parity;          // amax slot written by the current step's LM head
+  int use_override;    // 1: the next step's token is tok_override
+  uint32_t tok_override;
+  int prompt_len;      // positions < prompt_len take their token from the prompt buffer
+  int pad[2];
+  unsigned long long amax[2];  // (order_key(logit) << 32) | index, max-reduced
+};
+
+struct GemvArgs {
+  const uint8_t* w0 = nullptr;
+  const uint8_t* w1 = nullptr;  // second matrix (EPI_SWIGLU)
+  size_t row_stride = 0;        // bytes per weight row
+  int K = 0, N = 0;             // N = rows of this launch
+  int row0 = 0;                 // logical row index of this launch's row 0 (EPI_ROPE_QKV)
+  const float* x = nullptr;
+  const float* norm_w = nullptr;
+  float eps = 0.f;
+  int prologue = PRO_PLAIN, epilogue = EPI_STORE;
+  float* y = nullptr;
+  const float* resid = nullptr;
+  // EPI_ROPE_QKV
+  int qd = 0, kd = 0, hd = 0, max_ctx = 0;
+  const float* rope_cos = nullptr;
+  const float* rope_sin = nullptr;
+  uint16_t* kcache = nullptr;
+  uint16_t* vcache = nullptr;
+  const StepState* state = nullptr;  // position/parity source (nullptr: pos_host / slot 0)
+  int pos_host = 0;
+  // EPI_ARGMAX
+  unsigned long long* amax = nullptr;  // slot array; slot = state ? amax[state->parity] : amax[0]
+};
+
+// Chooses the lane layout for K and launches.  wtype in {Q4_K, Q6_K, Q8_0}.
+int launch_gemv_q8(const tpt_ctx* ctx, int wtype, const GemvArgs& a, hipStream_t s);
+int launch_gemv_f32(int wtype, const uint8_t* w, const float* x, float* y, int K, int N,
+                    hipStream_t s);
+
+int launch_dequant(int type, const void* w, float* y, int64_t n, hipStream_t s);
+int launch_rmsnorm(const float* x, const float* w, float* y, int n, float eps, hipStream_t s);
+int launch_rope(float* x, int n_heads, int hd, int pos, const float* c, const float* sn,
+                hipStream_t s);
+int launch_copy(void* dst, const void* src, size_t bytes, hipStream_t s);
+int launch_argmax(const float* logits, int64_t n, unsigned long long* slot, hipStream_t s);
+
+struct AttnArgs {
+  const float* q = nullptr;
+  const uint16_t* kc = nullptr;  // [nkv][L_stride][hd]
+  const uint16_t* vc = nullptr;
+  float* o = nullptr;
+  int nq = 0, nkv = 0, hd = 0, L_stride = 0;
+  int L_host = 0;                    // used when state == nullptr
+  const StepState* state = nullptr;  // L = state->pos + 1
+  int n_chunks = 0;
+  float* part = nullptr;             // [nkv][n_chunks][G][hd + 2]
+  unsigned int* counters = nullptr;  // [nkv], zero on entry, left zero on exit
+};
+int attn_part_floats(int nq, int nkv, int hd, int n_chunks);
+int attn_default_chunks(int L, int nkv);
+int launch_attn_decode(const AttnArgs& a, hipStream_t s);
+
+// Start of a decode step: pick the token, embed it (x = dequant(token_embd[tok])), advance the
+// step state and clear the amax slot the LM head will write.
+int launch_step_begin(StepState* st, const uint32_t* prompt, int embd_type,
+                      const uint8_t* embd, size_t embd_row_bytes, int H, int vocab, float* x,
+                      uint32_t* tok_log, hipStream_t s);
+
+}  // namespace tpt

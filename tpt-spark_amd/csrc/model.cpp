@@ -1,0 +1,619 @@
+// Device-resident Llama model: GGUF upload, decode step, prefill, greedy decode loop.
+//
+// Replaces load_gguf_to_vram (src-tauri/src/engine/wgpu_loader.rs:87-201), KvCache
+// (wgpu_kvcache.rs:15-79) and the per-token run_forward_pass (wgpu_engine.rs:339-490).  The
+// forward pass restates candle's quantized_llama (the reference CandleEngine's model):
+//   x = embed(tok); per layer: x += Wo . attn(rope(Wq.n(x)), rope(Wk.n(x)), Wv.n(x));
+//   x += W2 . (silu(W1.n'(x)) * W3.n'(x)); logits = Wout . n_out(x)
+// with the residual adds the wgpu engine omits (wgpu_engine.rs:443,474).  One decode step is
+// 2 + 5 * n_layers kernels (step begin, per layer QKV+RoPE+KV append / attention / Wo+residual /
+// gate|up+SiLU / down+residual, LM head + argmax), captured once into a HIP graph and replayed
+// for every token: position, token source and argmax slot live in a device StepState.
+#include "model.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <cstddef>
+
+using namespace tpt;
+
+namespace {
+
+bool matrix_type_ok(int t) {
+  return t == TPT_TYPE_Q4_K || t == TPT_TYPE_Q6_K || t == TPT_TYPE_Q8_0;
+}
+
+const char* type_name(int t) {
+  switch (t) {
+    case TPT_TYPE_F32: return "F32";
+    case TPT_TYPE_F16: return "F16";
+    case TPT_TYPE_Q8_0: return "Q8_0";
+    case TPT_TYPE_Q4_K: return "Q4_K";
+    case TPT_TYPE_Q6_K: return "Q6_K";
+  }
+  return "unsupported";
+}
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace
+
+tpt_model::~tpt_model() {
+  if (ctx) (void)hipSetDevice(ctx->device);
+  if (stream) (void)hipStreamSynchronize(stream);
+  for (auto& kv : graphs) (void)hipGraphExecDestroy(kv.second);
+  graphs.clear();
+  if (arena) (void)hipFree(arena);
+  if (runtime) (void)hipFree(runtime);
+  if (st_host) (void)hipHostFree(st_host);
+  if (ids_host) (void)hipHostFree(ids_host);
+}
+
+int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, tpt_progress_fn progress,
+                    void* user) {
+  ctx = c;
+  stream = c->stream;
+  path = gguf_path;
+  GgufFile f;
+  int rc = f.open(gguf_path);
+  if (rc) return rc;
+
+  // ---- metadata (extract_meta, wgpu_loader.rs:305-406; arch check as CandleEngine::load,
+  //      candle_engine.rs:146-156: the Llama-dense families this engine implements)
+  std::string arch = "llama";
+  f.get_str("general.architecture", &arch);
+  if (arch != "llama" && arch != "mistral")
+    return fail(TPT_ERR_UNSUPPORTED, "Architecture '" + arch + "' is not supported by engine-hip. Supported: llama, mistral.");
+  const std::string a = arch;
+  uint64_t u;
+  float fv;
+  desc = tpt_model_desc{};
+  snprintf(desc.architecture, sizeof desc.architecture, "%s", arch.c_str());
+  desc.context_length = f.get_u64(a + ".context_length", &u) ? (int)u : 4096;
+  desc.n_layers = f.get_u64(a + ".block_count", &u) ? (int)u : 32;
+  desc.n_heads = f.get_u64(a + ".attention.head_count", &u) ? (int)u : 32;
+  desc.n_kv_heads = f.get_u64(a + ".attention.head_count_kv", &u) ? (int)u : desc.n_heads;
+  desc.embed = f.get_u64(a + ".embedding_length", &u) ? (int)u : 4096;
+  desc.rope_base = f.get_f32(a + ".rope.freq_base", &fv) ? fv : 10000.f;
+  desc.rms_eps = f.get_f32(a + ".attention.layer_norm_rms_epsilon", &fv) ? fv : 1e-5f;
+  desc.rope_scale = 1.f;  // candle's quantized_llama applies no RoPE scaling
+  if (desc.n_heads <= 0 || desc.n_kv_heads <= 0 || desc.embed % desc.n_heads || desc.n_heads % desc.n_kv_heads)
+    return fail(TPT_ERR_FORMAT, "inconsistent head counts in GGUF metadata");
+  desc.head_dim = desc.embed / desc.n_heads;
+  const int rope_dim = f.get_u64(a + ".rope.dimension_count", &u) ? (int)u : desc.head_dim;
+  if (rope_dim != desc.head_dim)
+    return fail(TPT_ERR_UNSUPPORTED, "partial rotary embeddings (rope.dimension_count != head_dim) are not supported");
+  const int H = desc.embed, hd = desc.head_dim, nq = desc.n_heads, nkv = desc.n_kv_heads;
+  const int qd = nq * hd, kd = nkv * hd;
+
+  // ---- tensors
+  auto need = [&](const std::string& name, int64_t ne0, int64_t ne1, const GgufTensor** out) -> int {
+    const GgufTensor* t = f.find(name);
+    if (!t) return fail(TPT_ERR_FORMAT, "missing tensor " + name);
+    if (type_bytes(t->type) == 0 || !t->data)
+      return fail(TPT_ERR_UNSUPPORTED, "tensor " + name + " has ggml type " + std::to_string(t->type) + ", which engine-hip does not read");
+    if (t->ne[0] != ne0 || (ne1 >= 0 && t->ne[1] != ne1))
+      return fail(TPT_ERR_FORMAT, "tensor " + name + " has an unexpected shape");
+    *out = t;
+    return TPT_OK;
+  };
+  const GgufTensor *te, *to = nullptr, *ton;
+  if ((rc = need("token_embd.weight", H, -1, &te))) return rc;
+  desc.vocab = (int)te->ne[1];
+  if (f.find("output.weight")) {
+    if ((rc = need("output.weight", H, desc.vocab, &to))) return rc;
+  } else {
+    to = te;  // quantized_llama falls back to tok_embeddings
+  }
+  if ((rc = need("output_norm.weight", H, -1, &ton))) return rc;
+  if (ton->type != TPT_TYPE_F32) return fail(TPT_ERR_UNSUPPORTED, "output_norm must be F32");
+  if (!matrix_type_ok(to->type)) return fail(TPT_ERR_UNSUPPORTED, std::string("output.weight type ") + type_name(to->type) + " is not supported");
+  const GgufTensor* g0 = f.find("blk.0.ffn_gate.weight");
+  if (!g0) return fail(TPT_ERR_FORMAT, "missing tensor blk.0.ffn_gate.weight");
+  uint64_t ffn_meta;
+  desc.ffn = f.get_u64(a + ".feed_forward_length", &ffn_meta) ? (int)ffn_meta : (int)g0->ne[1];
+
+  struct LT { const GgufTensor *q, *k, *v, *o, *g, *u, *d, *an, *fn; };
+  std::vector<LT> lt(desc.n_layers);
+  for (int l = 0; l < desc.n_layers; l++) {
+    const std::string p = "blk." + std::to_string(l) + ".";
+    LT& t = lt[l];
+    if ((rc = need(p + "attn_q.weight", H, qd, &t.q)) || (rc = need(p + "attn_k.weight", H, kd, &t.k)) ||
+        (rc = need(p + "attn_v.weight", H, kd, &t.v)) || (rc = need(p + "attn_output.weight", qd, H, &t.o)) ||
+        (rc = need(p + "ffn_gate.weight", H, desc.ffn, &t.g)) || (rc = need(p + "ffn_up.weight", H, desc.ffn, &t.u)) ||
+        (rc = need(p + "ffn_down.weight", desc.ffn, H, &t.d)) || (rc = need(p + "attn_norm.weight", H, -1, &t.an)) ||
+        (rc = need(p + "ffn_norm.weight", H, -1, &t.fn)))
+      return rc;
+    for (const GgufTensor* m : {t.q, t.k, t.v, t.o, t.g, t.u, t.d})
+      if (!matrix_type_ok(m->type))
+        return fail(TPT_ERR_UNSUPPORTED, "tensor " + m->name + " has type " + type_name(m->type) + "; engine-hip reads Q4_K, Q6_K and Q8_0 matrices");
+    if (t.an->type != TPT_TYPE_F32 || t.fn->type != TPT_TYPE_F32) return fail(TPT_ERR_UNSUPPORTED, "norm weights must be F32");
+    if (t.g->type != t.u->type)
+      return fail(TPT_ERR_UNSUPPORTED, "ffn_gate and ffn_up of different types are not supported yet");
+    if (H % 256 || desc.ffn % 256 || qd % 256) return fail(TPT_ERR_UNSUPPORTED, "dimensions must be multiples of 256");
+  }
+
+  // ---- HBM layout: per layer q|k|v adjacent (one GEMV over qd + 2 kd rows), then the rest
+  std::vector<std::pair<const GgufTensor*, size_t>> plan;  // tensor, arena offset
+  size_t off = 0;
+  auto place = [&](const GgufTensor* t, size_t align) {
+    off = align_up(off, align);
+    plan.push_back({t, off});
+    off += t->bytes;
+  };
+  for (auto& t : lt) {
+    place(t.q, 256);
+    place(t.k, 1);
+    place(t.v, 1);
+    place(t.o, 256);
+    place(t.g, 256);
+    place(t.u, 256);
+    place(t.d, 256);
+    place(t.an, 256);
+    place(t.fn, 256);
+  }
+  place(te, 256);
+  if (to != te) place(to, 256);
+  place(ton, 256);
+  arena_bytes = align_up(off, 256);
+  TPT_HIP(hipSetDevice(c->device));
+  TPT_HIP(hipMalloc((void**)&arena, arena_bytes));
+
+  // ---- upload, blocks unchanged, through two pinned staging buffers
+  const size_t SB = 64u << 20;
+  uint8_t* stage[2] = {nullptr, nullptr};
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  TPT_HIP(hipHostMalloc((void**)&stage[0], SB));
+  TPT_HIP(hipHostMalloc((void**)&stage[1], SB));
+  TPT_HIP(hipEventCreate(&ev[0]));
+  TPT_HIP(hipEventCreate(&ev[1]));
+  int which = 0;
+  bool used[2] = {false, false};
+  uint32_t done = 0;
+  const uint32_t total = (uint32_t)plan.size();
+  hipError_t he = hipSuccess;
+  for (auto& pt : plan) {
+    const uint8_t* src = pt.first->data;
+    size_t left = pt.first->bytes, doff = pt.second;
+    while (left && he == hipSuccess) {
+      const size_t n = std::min(left, SB);
+      if (used[which]) he = hipEventSynchronize(ev[which]);
+      if (he != hipSuccess) break;
+      memcpy(stage[which], src, n);
+      he = hipMemcpyAsync(arena + doff, stage[which], n, hipMemcpyHostToDevice, stream);
+      if (he == hipSuccess) he = hipEventRecord(ev[which], stream);
+      used[which] = true;
+      which ^= 1;
+      src += n;
+      doff += n;
+      left -= n;
+    }
+    if (he != hipSuccess) break;
+    done++;
+    if (progress) progress(user, done, total);  // on_progress(done, total), wgpu_loader.rs:184-187
+  }
+  if (he == hipSuccess) he = hipStreamSynchronize(stream);
+  (void)hipEventDestroy(ev[0]);
+  (void)hipEventDestroy(ev[1]);
+  (void)hipHostFree(stage[0]);
+  (void)hipHostFree(stage[1]);
+  if (he != hipSuccess) return hip_fail(he, "weight upload", __FILE__, __LINE__);
+
+  auto dev = [&](const GgufTensor* t) -> const uint8_t* {
+    for (auto& pt : plan)
+      if (pt.first == t) return arena + pt.second;
+    return nullptr;
+  };
+  layers.resize(desc.n_layers);
+  uint64_t step_bytes = 0;
+  for (int l = 0; l < desc.n_layers; l++) {
+    Layer& L = layers[l];
+    const LT& t = lt[l];
+    L.q = dev(t.q); L.k = dev(t.k); L.v = dev(t.v); L.o = dev(t.o);
+    L.gate = dev(t.g); L.up = dev(t.u); L.down = dev(t.d);
+    L.attn_norm = (const float*)dev(t.an);
+    L.ffn_norm = (const float*)dev(t.fn);
+    L.tq = t.q->type; L.tk = t.k->type; L.tv = t.v->type; L.to = t.o->type;
+    L.tg = t.g->type; L.tu = t.u->type; L.td = t.d->type;
+    L.qkv_adjacent = L.tq == L.tk && L.tk == L.tv && L.k == L.q + t.q->bytes && L.v == L.k + t.k->bytes;
+    for (const GgufTensor* m : {t.q, t.k, t.v, t.o, t.g, t.u, t.d, t.an, t.fn}) step_bytes += m->bytes;
+  }
+  embd = dev(te);
+  embd_type = te->type;
+  embd_row = row_bytes(te->type, H);
+  out = dev(to);
+  out_type = to->type;
+  out_norm = (const float*)dev(ton);
+  step_bytes += to->bytes + ton->bytes + embd_row;
+  desc.weight_bytes = arena_bytes;
+  desc.decode_bytes_per_token = step_bytes;
+  desc.type_q = lt[0].q->type; desc.type_k = lt[0].k->type; desc.type_v = lt[0].v->type;
+  desc.type_o = lt[0].o->type; desc.type_gate = lt[0].g->type; desc.type_up = lt[0].u->type;
+  desc.type_down = lt[0].d->type; desc.type_embd = te->type; desc.type_out = to->type;
+
+  // ---- runtime state
+  const int max_ctx = max_ctx_req > 0 ? max_ctx_req : desc.context_length;
+  if (max_ctx <= 0) return fail(TPT_ERR_INVALID, "max_ctx must be positive");
+  desc.max_ctx = max_ctx;
+  attn_max_chunks = attn_default_chunks(max_ctx, nkv);
+  for (int b = 64; b < max_ctx * 2; b *= 2) attn_max_chunks = std::max(attn_max_chunks, attn_default_chunks(b, nkv));
+  const size_t kv_elems = (size_t)desc.n_layers * 2 * nkv * (size_t)max_ctx * hd;
+  size_t ro = 0;
+  auto carve = [&](size_t bytes) { size_t o = ro; ro = align_up(ro + bytes, 256); return o; };
+  const size_t o_kv = carve(kv_elems * 2), o_x = carve((size_t)H * 4), o_q = carve((size_t)qd * 4),
+               o_at = carve((size_t)qd * 4), o_h = carve((size_t)desc.ffn * 4),
+               o_lg = carve((size_t)desc.vocab * 4), o_rc = carve((size_t)max_ctx * hd / 2 * 4),
+               o_rs = carve((size_t)max_ctx * hd / 2 * 4), o_st = carve(sizeof(StepState)),
+               o_pr = carve((size_t)max_ctx * 4), o_tl = carve((size_t)max_ctx * 4),
+               o_ap = carve((size_t)attn_part_floats(nq, nkv, hd, attn_max_chunks) * 4),
+               o_ac = carve((size_t)nkv * 4);
+  TPT_HIP(hipMalloc(&runtime, ro));
+  uint8_t* R = (uint8_t*)runtime;
+  kv = (uint16_t*)(R + o_kv);
+  x = (float*)(R + o_x);
+  qbuf = (float*)(R + o_q);
+  attn = (float*)(R + o_at);
+  hbuf = (float*)(R + o_h);
+  logits = (float*)(R + o_lg);
+  rope_cos = (float*)(R + o_rc);
+  rope_sin = (float*)(R + o_rs);
+  st = (StepState*)(R + o_st);
+  prompt_dev = (uint32_t*)(R + o_pr);
+  tok_log = (uint32_t*)(R + o_tl);
+  attn_part = (float*)(R + o_ap);
+  attn_cnt = (unsigned int*)(R + o_ac);
+  TPT_HIP(hipMemsetAsync(runtime, 0, ro, stream));  // load time, outside any graph
+
+  // RoPE tables exactly as quantized_llama::precomput_freqs_cis: f32 theta = 1/base^(2i/d)
+  // (powf), angle = (f32)pos * theta, cosf/sinf of the host libm.
+  {
+    const int half = hd / 2;
+    std::vector<float> theta(half), tc((size_t)max_ctx * half), ts((size_t)max_ctx * half);
+    for (int i = 0; i < half; i++) theta[i] = 1.f / powf(desc.rope_base, (float)(2 * i) / (float)hd);
+    for (int p = 0; p < max_ctx; p++)
+      for (int i = 0; i < half; i++) {
+        const float ang = (float)p * theta[i];
+        tc[(size_t)p * half + i] = cosf(ang);
+        ts[(size_t)p * half + i] = sinf(ang);
+      }
+    TPT_HIP(hipMemcpy(rope_cos, tc.data(), tc.size() * 4, hipMemcpyHostToDevice));
+    TPT_HIP(hipMemcpy(rope_sin, ts.data(), ts.size() * 4, hipMemcpyHostToDevice));
+  }
+  TPT_HIP(hipHostMalloc((void**)&st_host, sizeof(StepState)));
+  TPT_HIP(hipHostMalloc((void**)&ids_host, (size_t)max_ctx * 4));
+  const char* ev_graph = getenv("TPT_HIP_GRAPHS");
+  use_graphs = !(ev_graph && ev_graph[0] == '0');
+  TPT_HIP(hipStreamSynchronize(stream));
+  return TPT_OK;
+}
+
+int tpt_model::chunks_for(int L) const {
+  int b = 64;
+  while (b < L) b *= 2;
+  return std::min(attn_default_chunks(b, desc.n_kv_heads), attn_max_chunks);
+}
+
+int tpt_model::enqueue_step(int n_chunks, bool lm_head) {
+  const int H = desc.embed, hd = desc.head_dim, nq = desc.n_heads, nkv = desc.n_kv_heads;
+  const int qd = nq * hd, kd = nkv * hd, F = desc.ffn, mc = desc.max_ctx;
+  int rc = launch_step_begin(st, prompt_dev, embd_type, embd, embd_row, H, desc.vocab, x, tok_log, stream);
+  if (rc) return rc;
+  const size_t layer_kv = (size_t)2 * nkv * mc * hd;
+  for (int l = 0; l < desc.n_layers; l++) {
+    const Layer& L = layers[l];
+    uint16_t* kc = kv + (size_t)l * layer_kv;
+    uint16_t* vc = kc + (size_t)nkv * mc * hd;
+    // norm -> Q|K|V GEMV -> RoPE -> q buffer / fp16 KV append at state->pos
+    GemvArgs g;
+    g.K = H;
+    g.x = x;
+    g.norm_w = L.attn_norm;
+    g.eps = desc.rms_eps;
+    g.prologue = PRO_RMSNORM;
+    g.epilogue = EPI_ROPE_QKV;
+    g.y = qbuf;
+    g.qd = qd;
+    g.kd = kd;
+    g.hd = hd;
+    g.max_ctx = mc;
+    g.rope_cos = rope_cos;
+    g.rope_sin = rope_sin;
+    g.kcache = kc;
+    g.vcache = vc;
+    g.state = st;
+    if (L.qkv_adjacent) {
+      g.w0 = L.q;
+      g.row_stride = row_bytes(L.tq, H);
+      g.N = qd + 2 * kd;
+      if ((rc = launch_gemv_q8(ctx, L.tq, g, stream))) return rc;
+    } else {
+      const uint8_t* ws[3] = {L.q, L.k, L.v};
+      const int ts[3] = {L.tq, L.tk, L.tv}, ns[3] = {qd, kd, kd}, r0[3] = {0, qd, qd + kd};
+      for (int i = 0; i < 3; i++) {
+        g.w0 = ws[i];
+        g.row_stride = row_bytes(ts[i], H);
+        g.N = ns[i];
+        g.row0 = r0[i];
+        if ((rc = launch_gemv_q8(ctx, ts[i], g, stream))) return rc;
+      }
+    }
+    // attention over positions 0..state->pos
+    AttnArgs at;
+    at.q = qbuf;
+    at.kc = kc;
+    at.vc = vc;
+    at.o = attn;
+    at.nq = nq;
+    at.nkv = nkv;
+    at.hd = hd;
+    at.L_stride = mc;
+    at.state = st;
+    at.n_chunks = n_chunks;
+    at.part = attn_part;
+    at.counters = attn_cnt;
+    if ((rc = launch_attn_decode(at, stream))) return rc;
+    // x += Wo . attn
+    GemvArgs wo;
+    wo.w0 = L.o;
+    wo.row_stride = row_bytes(L.to, qd);
+    wo.K = qd;
+    wo.N = H;
+    wo.x = attn;
+    wo.epilogue = EPI_RESID;
+    wo.y = x;
+    wo.resid = x;
+    if ((rc = launch_gemv_q8(ctx, L.to, wo, stream))) return rc;
+    // h = silu(W1 . n(x)) * (W3 . n(x))
+    GemvArgs gu;
+    gu.w0 = L.gate;
+    gu.w1 = L.up;
+    gu.row_stride = row_bytes(L.tg, H);
+    gu.K = H;
+    gu.N = F;
+    gu.x = x;
+    gu.norm_w = L.ffn_norm;
+    gu.eps = desc.rms_eps;
+    gu.prologue = PRO_RMSNORM;
+    gu.epilogue = EPI_SWIGLU;
+    gu.y = hbuf;
+    if ((rc = launch_gemv_q8(ctx, L.tg, gu, stream))) return rc;
+    // x += W2 . h
+    GemvArgs dn;
+    dn.w0 = L.down;
+    dn.row_stride = row_bytes(L.td, F);
+    dn.K = F;
+    dn.N = H;
+    dn.x = hbuf;
+    dn.epilogue = EPI_RESID;
+    dn.y = x;
+    dn.resid = x;
+    if ((rc = launch_gemv_q8(ctx, L.td, dn, stream))) return rc;
+  }
+  if (lm_head) {
+    GemvArgs lh;
+    lh.w0 = out;
+    lh.row_stride = row_bytes(out_type, H);
+    lh.K = H;
+    lh.N = desc.vocab;
+    lh.x = x;
+    lh.norm_w = out_norm;
+    lh.eps = desc.rms_eps;
+    lh.prologue = PRO_RMSNORM;
+    lh.epilogue = EPI_ARGMAX;
+    lh.y = logits;
+    lh.amax = (unsigned long long*)((char*)st + offsetof(StepState, amax));  // device address
+    lh.state = st;
+    if ((rc = launch_gemv_q8(ctx, out_type, lh, stream))) return rc;
+  }
+  return TPT_OK;
+}
+
+int tpt_model::launch_step(int L, bool lm_head) {
+  if (L > desc.max_ctx) return fail(TPT_ERR_STATE, "context length exhausted");
+  const int nch = chunks_for(L);
+  if (!use_graphs || !lm_head) return enqueue_step(nch, lm_head);
+  auto it = graphs.find(nch);
+  if (it == graphs.end()) {
+    hipGraph_t g = nullptr;
+    TPT_HIP(hipStreamBeginCapture(stream, hipStreamCaptureModeRelaxed));
+    int rc = enqueue_step(nch, true);
+    hipError_t e = hipStreamEndCapture(stream, &g);
+    if (rc) {
+      if (g) (void)hipGraphDestroy(g);
+      return rc;
+    }
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture", __FILE__, __LINE__);
+    hipGraphExec_t ex = nullptr;
+    e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate", __FILE__, __LINE__);
+    it = graphs.emplace(nch, ex).first;
+  }
+  TPT_HIP(hipGraphLaunch(it->second, stream));
+  return TPT_OK;
+}
+
+int tpt_model::set_state(int next_pos, int prompt_len, int use_override, uint32_t tok) {
+  memset(st_host, 0, sizeof(StepState));
+  st_host->next_pos = next_pos;
+  st_host->prompt_len = prompt_len;
+  st_host->use_override = use_override;
+  st_host->tok_override = tok;
+  TPT_HIP(hipMemcpyAsync(st, st_host, sizeof(StepState), hipMemcpyHostToDevice, stream));
+  // the pinned source must not change before the copy runs
+  TPT_HIP(hipStreamSynchronize(stream));
+  return TPT_OK;
+}
+
+int tpt_model::read_state(StepState* out_state) {
+  TPT_HIP(hipMemcpyAsync(st_host, st, sizeof(StepState), hipMemcpyDeviceToHost, stream));
+  TPT_HIP(hipStreamSynchronize(stream));
+  *out_state = *st_host;
+  return TPT_OK;
+}
+
+int tpt_model::prefill(const uint32_t* ids, int n, int pos0, uint32_t* next_out, float* logits_out) {
+  if (n <= 0 || pos0 < 0 || pos0 + n > desc.max_ctx) return fail(TPT_ERR_INVALID, "prefill: positions out of range");
+  for (int i = 0; i < n; i++)
+    if (ids[i] >= (uint32_t)desc.vocab) return fail(TPT_ERR_INVALID, "prefill: token id out of vocabulary");
+  memcpy(ids_host + pos0, ids, (size_t)n * 4);
+  TPT_HIP(hipMemcpyAsync(prompt_dev + pos0, ids_host + pos0, (size_t)n * 4, hipMemcpyHostToDevice, stream));
+  int rc = set_state(pos0, pos0 + n, 0, 0);
+  if (rc) return rc;
+  for (int i = 0; i < n; i++)
+    if ((rc = launch_step(pos0 + i + 1, true))) return rc;
+  StepState s;
+  if ((rc = read_state(&s))) return rc;
+  if (next_out) *next_out = (uint32_t)(s.amax[s.parity] & 0xffffffffull);
+  if (logits_out) {
+    TPT_HIP(hipMemcpyAsync(logits_out, logits, (size_t)desc.vocab * 4, hipMemcpyDeviceToHost, stream));
+    TPT_HIP(hipStreamSynchronize(stream));
+  }
+  return TPT_OK;
+}
+
+int tpt_model::decode_stream(uint32_t first, int pos0, int n_steps, StepFn fn, void* user,
+                             int* n_delivered) {
+  *n_delivered = 0;
+  if (n_steps <= 0) return TPT_OK;
+  if (pos0 < 0 || pos0 + n_steps > desc.max_ctx) return fail(TPT_ERR_INVALID, "decode: positions out of range");
+  if (first >= (uint32_t)desc.vocab) return fail(TPT_ERR_INVALID, "decode: token id out of vocabulary");
+  int rc = set_state(pos0, 0, 1, first);
+  if (rc) return rc;
+  // Steps go out in batches; while batch b runs, the host reads the tokens batch b-1 produced
+  // (step s's token is logged by step s+1's begin kernel) and hands them to fn in order.
+  const int BATCH = 16;
+  std::vector<uint32_t> log((size_t)n_steps + 1);
+  std::vector<hipEvent_t> evs;
+  int launched = 0, delivered = 0;
+  bool stop = false;
+  auto deliver = [&](int upto) -> int {  // tokens produced by steps [delivered, upto)
+    if (upto > delivered) {
+      TPT_HIP(hipMemcpy(log.data() + delivered, tok_log + pos0 + 1 + delivered,
+                        (size_t)(upto - delivered) * 4, hipMemcpyDeviceToHost));
+      for (int s = delivered; s < upto && !stop; s++) {
+        delivered = s + 1;
+        if (fn(user, s, log[s])) stop = true;
+      }
+    }
+    return TPT_OK;
+  };
+  while (launched < n_steps && !stop) {
+    const int nb = std::min(BATCH, n_steps - launched);
+    for (int i = 0; i < nb && rc == TPT_OK; i++) rc = launch_step(pos0 + launched + i + 1, true);
+    if (rc) break;
+    launched += nb;
+    hipEvent_t e;
+    TPT_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    TPT_HIP(hipEventRecord(e, stream));
+    evs.push_back(e);
+    if (evs.size() >= 2) {
+      TPT_HIP(hipEventSynchronize(evs[evs.size() - 2]));
+      if ((rc = deliver(launched - nb - 1))) break;
+    }
+  }
+  hipError_t e = hipStreamSynchronize(stream);
+  for (hipEvent_t ev : evs) (void)hipEventDestroy(ev);
+  if (rc) return rc;
+  if (e != hipSuccess) return hip_fail(e, "decode", __FILE__, __LINE__);
+  if (!stop && (rc = deliver(launched - 1))) return rc;
+  if (!stop && delivered == launched - 1) {
+    StepState s;
+    if ((rc = read_state(&s))) return rc;
+    const uint32_t last = (uint32_t)(s.amax[s.parity] & 0xffffffffull);
+    delivered = launched;
+    fn(user, launched - 1, last);
+  }
+  *n_delivered = delivered;
+  return TPT_OK;
+}
+
+namespace {
+struct GreedyCollect {
+  uint32_t* out;
+  int64_t stop;
+  int n;
+};
+int greedy_collect(void* u, int s, uint32_t tok) {
+  GreedyCollect* g = (GreedyCollect*)u;
+  g->out[s] = tok;
+  g->n = s + 1;
+  return g->stop >= 0 && tok == (uint32_t)g->stop;
+}
+}  // namespace
+
+int tpt_model::decode_greedy(uint32_t first, int pos0, int n_steps, int64_t stop_tok, uint32_t* out_tok) {
+  GreedyCollect g{out_tok, stop_tok, 0};
+  int delivered = 0;
+  const int rc = decode_stream(first, pos0, n_steps, greedy_collect, &g, &delivered);
+  return rc ? rc : g.n;
+}
+
+// ------------------------------------------------------------------ C ABI
+
+extern "C" {
+
+int tpt_model_load(tpt_ctx* c, const char* gguf_path, int max_ctx, tpt_progress_fn progress,
+                   void* user, tpt_model** out) {
+  int rc = ctx_enter(c);
+  if (rc) return rc;
+  if (!gguf_path || !out) return fail(TPT_ERR_INVALID, "null argument");
+  tpt_model* m = new tpt_model();
+  rc = m->load(c, gguf_path, max_ctx, progress, user);
+  if (rc) {
+    delete m;
+    return rc;
+  }
+  *out = m;
+  return TPT_OK;
+}
+
+int tpt_model_describe(const tpt_model* m, tpt_model_desc* out) {
+  if (!m || !out) return fail(TPT_ERR_INVALID, "null argument");
+  *out = m->desc;
+  return TPT_OK;
+}
+
+int tpt_model_destroy(tpt_model* m) {
+  delete m;
+  return TPT_OK;
+}
+
+int tpt_model_prefill(tpt_model* m, const uint32_t* ids, int n, int pos0, uint32_t* next_out,
+                      float* logits_out) {
+  if (!m || !ids) return fail(TPT_ERR_INVALID, "null argument");
+  int rc = ctx_enter(m->ctx);
+  if (rc) return rc;
+  return m->prefill(ids, n, pos0, next_out, logits_out);
+}
+
+int tpt_model_decode_step(tpt_model* m, uint32_t tok, int pos, uint32_t* next_out,
+                          float* logits_out) {
+  if (!m) return fail(TPT_ERR_INVALID, "null argument");
+  int rc = ctx_enter(m->ctx);
+  if (rc) return rc;
+  return m->prefill(&tok, 1, pos, next_out, logits_out);
+}
+
+int tpt_model_decode_greedy(tpt_model* m, uint32_t first, int pos0, int n_steps,
+                            int64_t stop_token, uint32_t* tokens_out) {
+  if (!m || (!tokens_out && n_steps > 0)) return fail(TPT_ERR_INVALID, "null argument");
+  int rc = ctx_enter(m->ctx);
+  if (rc) return rc;
+  return m->decode_greedy(first, pos0, n_steps, stop_token, tokens_out);
+}
+
+int tpt_model_hidden(tpt_model* m, float* out_host) {
+  if (!m || !out_host) return fail(TPT_ERR_INVALID, "null argument");
+  int rc = ctx_enter(m->ctx);
+  if (rc) return rc;
+  TPT_HIP(hipMemcpyAsync(out_host, m->x, (size_t)m->desc.embed * 4, hipMemcpyDeviceToHost, m->stream));
+  TPT_HIP(hipStreamSynchronize(m->stream));
+  return TPT_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,64 @@
+// Device-resident Llama model for bs=1 decode (host side).
+#pragma once
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "gguf.h"
+#include "kernels.h"
+
+struct tpt_model {
+  struct Layer {
+    const uint8_t *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
+    const uint8_t *gate = nullptr, *up = nullptr, *down = nullptr;
+    const float *attn_norm = nullptr, *ffn_norm = nullptr;
+    int tq = 0, tk = 0, tv = 0, to = 0, tg = 0, tu = 0, td = 0;
+    bool qkv_adjacent = false;  // q, k, v rows contiguous in HBM and of one type
+  };
+
+  tpt_ctx* ctx = nullptr;  // not owned
+  hipStream_t stream = nullptr;
+  tpt_model_desc desc{};
+  std::string path;
+
+  uint8_t* arena = nullptr;  // all weights, blocks unchanged
+  size_t arena_bytes = 0;
+  std::vector<Layer> layers;
+  const uint8_t* embd = nullptr;
+  int embd_type = 0;
+  size_t embd_row = 0;
+  const uint8_t* out = nullptr;
+  int out_type = 0;
+  const float* out_norm = nullptr;
+
+  // runtime buffers
+  uint16_t* kv = nullptr;  // [layer][K|V][nkv][max_ctx][hd] fp16
+  float *x = nullptr, *qbuf = nullptr, *attn = nullptr, *hbuf = nullptr, *logits = nullptr;
+  float *rope_cos = nullptr, *rope_sin = nullptr;  // [max_ctx][hd/2]
+  tpt::StepState* st = nullptr;
+  uint32_t* prompt_dev = nullptr;  // [max_ctx] token ids by position
+  uint32_t* tok_log = nullptr;     // [max_ctx] token consumed at each position
+  float* attn_part = nullptr;
+  unsigned int* attn_cnt = nullptr;
+  int attn_max_chunks = 0;
+  void* runtime = nullptr;  // one allocation holding the buffers above
+
+  tpt::StepState* st_host = nullptr;  // pinned
+  uint32_t* ids_host = nullptr;       // pinned staging for prompt ids [max_ctx]
+  bool use_graphs = true;
+  std::map<int, hipGraphExec_t> graphs;  // by attention chunk count
+
+  ~tpt_model();
+  int load(tpt_ctx* c, const char* gguf_path, int max_ctx, tpt_progress_fn progress, void* user);
+  int enqueue_step(int n_chunks, bool lm_head);
+  int launch_step(int L, bool lm_head);  // graph replay (or direct launches)
+  int chunks_for(int L) const;
+  int set_state(int next_pos, int prompt_len, int use_override, uint32_t tok);
+  int read_state(tpt::StepState* out);
+  int prefill(const uint32_t* ids, int n, int pos0, uint32_t* next_out, float* logits_out);
+  // fn(user, s, tok) receives the token step s produced, in order; non-zero stops the run.
+  typedef int (*StepFn)(void* user, int s, uint32_t tok);
+  int decode_stream(uint32_t first, int pos0, int n_steps, StepFn fn, void* user, int* n_delivered);
+  int decode_greedy(uint32_t first, int pos0, int n_steps, int64_t stop, uint32_t* out);
+};

@@ -1,0 +1,104 @@
+// Shared definitions of libtpthip: GGUF block layouts, device helpers, error plumbing.
+// All device code is compiled for gfx950 with -ffp-contract=off; fused multiply-adds are
+// written out explicitly (fmaf) where they are wanted, so every non-FMA expression keeps
+// the rounding of the CPU arithmetic it restates.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <string>
+
+#include "../../include/tpthip.h"
+
+namespace tpt {
+
+constexpr int QK_K = 256;
+constexpr int QK8_0 = 32;
+constexpr int WAVE = 64;
+
+// ggml block layouts (bytes are uploaded unchanged; these describe them).
+struct __attribute__((packed)) BlockQ4K { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[128]; };
+struct __attribute__((packed)) BlockQ6K { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; };
+struct __attribute__((packed)) BlockQ8_0 { uint16_t d; int8_t qs[32]; };
+static_assert(sizeof(BlockQ4K) == 144, "q4k");
+static_assert(sizeof(BlockQ6K) == 210, "q6k");
+static_assert(sizeof(BlockQ8_0) == 34, "q8_0");
+
+__host__ __device__ inline int type_block(int t) {
+  return t == TPT_TYPE_Q4_K || t == TPT_TYPE_Q6_K ? QK_K : t == TPT_TYPE_Q8_0 ? QK8_0 : 1;
+}
+__host__ __device__ inline int type_bytes(int t) {
+  return t == TPT_TYPE_Q4_K ? 144 : t == TPT_TYPE_Q6_K ? 210 : t == TPT_TYPE_Q8_0 ? 34
+         : t == TPT_TYPE_F16 ? 2 : t == TPT_TYPE_F32 ? 4 : 0;
+}
+inline size_t row_bytes(int t, int64_t k) { return (size_t)(k / type_block(t)) * type_bytes(t); }
+
+// ---------------------------------------------------------------- device helpers
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);  // v_cvt_f32_f16: exact
+}
+__device__ __forceinline__ uint16_t f2h(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);  // round to nearest even
+}
+
+template <typename T>
+__device__ __forceinline__ T ldg_u(const uint8_t* p) {  // unaligned-tolerant load
+  T v;
+  __builtin_memcpy(&v, p, sizeof(T));
+  return v;
+}
+
+__device__ __forceinline__ int sdot4(int a, int b, int c) {
+  return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, WAVE);
+  return v;
+}
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {  // sum over aligned groups of W lanes
+#pragma unroll
+  for (int o = W / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, WAVE);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+  return v;
+}
+
+// f32 total order key (f32::total_cmp) widened to an unsigned key: larger key = larger value.
+__device__ __forceinline__ uint32_t order_key(float f) {
+  uint32_t b = __builtin_bit_cast(uint32_t, f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// ---------------------------------------------------------------- errors
+
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int hip_fail(hipError_t e, const char* what, const char* file, int line);
+
+#define TPT_HIP(call)                                                   \
+  do {                                                                  \
+    hipError_t _e = (call);                                             \
+    if (_e != hipSuccess) return ::tpt::hip_fail(_e, #call, __FILE__, __LINE__); \
+  } while (0)
+
+}  // namespace tpt
+
+struct tpt_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  int n_cu = 0;
+  char name[256] = {0};
+};
+
+namespace tpt {
+int ctx_enter(tpt_ctx* c);  // hipSetDevice(c->device); status
+}
