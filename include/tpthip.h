@@ -95,11 +95,13 @@ int tpt_rope(tpt_ctx* ctx, float* x, int n_heads, int hd, int pos, const float* 
              const float* sin_t);
 
 /* Decode attention for one query position: o[Nq,hd] = softmax(q K^T / sqrt(hd)) V over the
- * first L positions of an fp16 cache laid out [Nkv][L_stride][hd] (GQA: head h reads kv
- * head h / (Nq/Nkv)).  Replaces attention.wgsl:31-170 (dispatch_attention,
- * wgpu_engine.rs:666-726).  n_chunks = 0 picks the split-K partition count. */
+ * first L positions of a cache laid out [Nkv][L_stride][hd] with elements of kv_type
+ * (TPT_TYPE_F16 or TPT_TYPE_F32; GQA: head h reads kv head h / (Nq/Nkv)).  Replaces
+ * attention.wgsl:31-170 (dispatch_attention, wgpu_engine.rs:666-726).  n_chunks = 0 picks the
+ * split-K partition count (at most 256 chunks of at most 1024 positions). */
 int tpt_attn_decode(tpt_ctx* ctx, const float* q, const void* k_cache, const void* v_cache,
-                    float* o, int nq, int nkv, int hd, int L, int L_stride, int n_chunks);
+                    int kv_type, float* o, int nq, int nkv, int hd, int L, int L_stride,
+                    int n_chunks);
 
 /* Greedy token of a logits vector: the last index among equal maxima under f32 total order
  * (candle LogitsProcessor::sample_argmax, used by sample_token wgpu_engine.rs:868-878). */
@@ -112,6 +114,10 @@ int tpt_argmax(tpt_ctx* ctx, const float* logits, int64_t n, uint32_t* out_host)
  * the 256 MB Infinity Cache); *ms_out = total event time of the launches. */
 int tpt_bench_gemv(tpt_ctx* ctx, int type, const void* const* weights, int n_weights,
                    const float* x, float* y, int K, int N, int iters, float* ms_out);
+/* iters launches of tpt_attn_decode over the same cache; *ms_out = total event time */
+int tpt_bench_attn(tpt_ctx* ctx, const float* q, const void* k_cache, const void* v_cache,
+                   int kv_type, float* o, int nq, int nkv, int hd, int L, int L_stride,
+                   int n_chunks, int iters, float* ms_out);
 /* iters launches of a plain vector copy of `bytes` (HBM calibration for PMC counters) */
 int tpt_bench_copy(tpt_ctx* ctx, void* dst, const void* src, size_t bytes, int iters,
                    float* ms_out);
@@ -126,6 +132,7 @@ typedef struct {
   int n_layers, n_heads, n_kv_heads, head_dim, embed, ffn, vocab;
   int context_length; /* from GGUF metadata */
   int max_ctx;        /* KV capacity actually allocated */
+  int kv_type;        /* KV cache element type: TPT_TYPE_F16 or TPT_TYPE_F32 */
   float rms_eps, rope_base, rope_scale;
   uint64_t weight_bytes; /* quantized bytes resident in HBM */
   uint64_t decode_bytes_per_token; /* weight bytes one decode step streams */
@@ -137,9 +144,10 @@ typedef struct {
 typedef void (*tpt_progress_fn)(void* user, uint32_t done, uint32_t total);
 
 /* mmap + validate + upload the k-quant blocks unchanged.  max_ctx <= 0 uses the GGUF
- * context_length. */
-int tpt_model_load(tpt_ctx* ctx, const char* gguf_path, int max_ctx, tpt_progress_fn progress,
-                   void* user, tpt_model** out);
+ * context_length.  kv_type TPT_TYPE_F16 (half the KV bytes) or TPT_TYPE_F32 (the cache candle
+ * keeps: the CandleEngine-exact mode). */
+int tpt_model_load(tpt_ctx* ctx, const char* gguf_path, int max_ctx, int kv_type,
+                   tpt_progress_fn progress, void* user, tpt_model** out);
 int tpt_model_describe(const tpt_model* m, tpt_model_desc* out);
 int tpt_model_destroy(tpt_model* m);
 
@@ -192,6 +200,8 @@ typedef struct {
 typedef int (*tpt_token_fn)(void* user, uint32_t token_id, int done);
 
 int tpt_engine_create(int device, tpt_engine** out);
+/* KV cache element type used by the next tpt_engine_load (default TPT_TYPE_F16). */
+int tpt_engine_set_kv_type(tpt_engine* e, int kv_type);
 int tpt_engine_destroy(tpt_engine* e);
 int tpt_engine_load(tpt_engine* e, const char* model_path, tpt_progress_fn progress, void* user,
                     tpt_model_info* info_out);

@@ -16,9 +16,18 @@ pytestmark = pytest.mark.gpu
 PROMPT = [11, 500, 7, 1023, 42, 99, 3]
 
 
+@pytest.fixture(scope="module", params=["f16", "f32"])
+def kv(request):
+    """KV cache element type: fp16 (the default engine layout) and f32 (candle's cache)."""
+    return request.param
+
+
+KV_TYPE = {"f16": tpthip.TYPE_F16, "f32": tpthip.TYPE_F32}
+
+
 @pytest.fixture(scope="module")
-def tiny_model(ctx, tiny_gguf):
-    m = tpthip.Model(ctx, tiny_gguf, max_ctx=256)
+def tiny_model(ctx, tiny_gguf, kv):
+    m = tpthip.Model(ctx, tiny_gguf, max_ctx=256, kv_type=KV_TYPE[kv])
     yield m
     m.close()
 
@@ -28,28 +37,32 @@ def tiny_oracle(tiny_gguf):
     return oracle.Model(tiny_gguf)
 
 
-def test_describe(tiny_model):
+def test_describe(tiny_model, kv):
     d = tiny_model.desc
     assert (d["n_layers"], d["embed"], d["n_heads"], d["n_kv_heads"], d["head_dim"], d["ffn"],
             d["vocab"]) == (2, 256, 4, 2, 64, 512, 1024)
     assert d["type_q"] == tpthip.TYPE_Q4_K and d["type_out"] == tpthip.TYPE_Q6_K
-    assert d["max_ctx"] == 256
+    assert d["max_ctx"] == 256 and d["kv_type"] == KV_TYPE[kv]
 
 
-def test_prefill_logits_match_oracle(tiny_model, tiny_oracle):
+def test_prefill_logits_match_oracle(tiny_model, tiny_oracle, kv):
+    """Same cache values as the oracle's mode: only f32 summation order differs (< 1e-3).
+    The f32 cache is candle's: its logits meet the candle bar (max-abs < 1e-2)."""
     nxt, lg = tiny_model.prefill(PROMPT, 0, logits=True)
-    tiny_oracle.reset(64, kv_f16=True)
-    ref16 = tiny_oracle.forward(PROMPT, 0)
-    tiny_oracle.reset(64, kv_f16=False)
-    ref32 = tiny_oracle.forward(PROMPT, 0)
-    assert np.abs(lg - ref16).max() < 1e-3  # same fp16 cache values: f32 order only
-    assert np.abs(lg - ref32).max() < 1e-2  # candle keeps an f32 cache
-    assert nxt == oracle.argmax(lg) == oracle.argmax(ref32)
+    tiny_oracle.reset(64, kv_f16=(kv == "f16"))
+    ref = tiny_oracle.forward(PROMPT, 0)
+    assert np.abs(lg - ref).max() < 1e-3
+    assert nxt == oracle.argmax(lg) == oracle.argmax(ref)
+    if kv == "f32":
+        tiny_oracle.reset(64, kv_f16=False)
+        assert np.abs(lg - tiny_oracle.forward(PROMPT, 0)).max() < 1e-2
 
 
-def test_greedy_tokens_match_oracle(tiny_model, tiny_oracle):
+def test_greedy_tokens_match_oracle(tiny_model, tiny_oracle, kv):
+    """40 greedy tokens identical to the oracle in the same cache mode; for the f32 cache that
+    is candle's greedy sequence (the bar: the first 32 identical, logits within 1e-2)."""
     n = 40
-    toks_ref, logits_ref = tiny_oracle.greedy(PROMPT, n, kv_f16=False, return_logits=(1, 32))
+    toks_ref, logits_ref = tiny_oracle.greedy(PROMPT, n, kv_f16=(kv == "f16"), return_logits=(1, 32))
     first = tiny_model.prefill(PROMPT, 0)
     got = [first] + tiny_model.decode_greedy(first, len(PROMPT), n - 1)
     assert got[:32] == toks_ref[:32]
@@ -101,7 +114,8 @@ def test_context_bounds(tiny_model):
 
 @pytest.fixture(scope="module")
 def engine(tiny_gguf):
-    e = tpthip.HipEngine(0)
+    """The engine in candle's cache mode (f32 KV), so its greedy output is candle's."""
+    e = tpthip.HipEngine(0, kv_type=tpthip.TYPE_F32)
     info = e.load(tiny_gguf)
     assert info.backend.startswith("hip-gfx")
     yield e

@@ -144,18 +144,19 @@ def test_rope_op(ctx):
     np.testing.assert_array_equal(y, oracle.rope_i(x, heads, hd, c[37], s[37]))
 
 
-def attention_case(ctx, nq, nkv, hd, L, seed):
-    """Config-4 chain: x ~ N(0,1) -> RMSNorm (w = 1, eps 1e-5) -> q (no projection) -> RoPE at
-    pos = L-1; cache K/V ~ N(0,1) stored fp16, the newest K row RoPE'd at L-1; causal."""
+def attention_case(ctx, nq, nkv, hd, L, seed, kv_dtype=np.float16):
+    """Decode-attention chain: x ~ N(0,1) -> RMSNorm (w = 1, eps 1e-5) -> q (no projection) ->
+    RoPE at pos = L-1; cache K/V ~ N(0,1) stored fp16 (or f32), the newest K row RoPE'd at
+    L-1; causal."""
     rng = np.random.default_rng(seed)
     base, eps = 500000.0, 1e-5
     cos_t, sin_t = oracle.rope_tables(hd, base, L)
     x = rng.standard_normal(nq * hd).astype(np.float32)
-    k = rng.standard_normal((nkv, L, hd)).astype(np.float16)
-    v = rng.standard_normal((nkv, L, hd)).astype(np.float16)
+    k = rng.standard_normal((nkv, L, hd)).astype(kv_dtype)
+    v = rng.standard_normal((nkv, L, hd)).astype(kv_dtype)
     knew = oracle.rope_i(rng.standard_normal(nkv * hd).astype(np.float32), nkv, hd,
                          cos_t[L - 1], sin_t[L - 1]).reshape(nkv, hd)
-    k[:, L - 1] = knew.astype(np.float16)
+    k[:, L - 1] = knew.astype(kv_dtype)
     ones = np.ones(nq * hd, np.float32)
     # GPU: rmsnorm -> rope -> attention
     xd = ctx.to_device(x)
@@ -163,7 +164,8 @@ def attention_case(ctx, nq, nkv, hd, L, seed):
     from tpthip import lib, check
     check(lib().tpt_rmsnorm(ctx.h, xd.ptr, ctx.to_device(ones).ptr, qn.ptr, nq * hd, eps))
     ctx.rope(qn, nq, hd, L - 1, ctx.to_device(cos_t), ctx.to_device(sin_t))
-    o = ctx.attn_decode(qn, ctx.to_device(k), ctx.to_device(v), nq, nkv, hd, L, L)
+    kvt = tpthip.TYPE_F32 if kv_dtype == np.float32 else tpthip.TYPE_F16
+    o = ctx.attn_decode(qn, ctx.to_device(k), ctx.to_device(v), nq, nkv, hd, L, L, kv_type=kvt)
     # oracle
     q = oracle.rope_i(oracle.rmsnorm(x, ones, eps), nq, hd, cos_t[L - 1], sin_t[L - 1])
     ref = oracle.attention(q, k.astype(np.float32), v.astype(np.float32), nq, nkv, hd, L)
@@ -183,7 +185,39 @@ def test_attention_mha_hd96(ctx, L):
     assert rel_l2(o, ref) < 1e-5
 
 
-@pytest.mark.parametrize("n_chunks", [1, 3, 64, 700])
+@pytest.mark.parametrize("nq,nkv,hd,L", [(32, 8, 128, 4096), (32, 32, 96, 777), (32, 8, 64, 2048),
+                                         (16, 2, 64, 1), (32, 4, 128, 32768)])
+def test_attention_f32_cache(ctx, nq, nkv, hd, L):
+    """candle's f32 cache layout through the same split-K kernel."""
+    o, ref = attention_case(ctx, nq, nkv, hd, L, seed=L + hd, kv_dtype=np.float32)
+    assert rel_l2(o, ref) < 1e-5
+
+
+def test_attention_single_position_is_v(ctx):
+    """Closed form: with one cached position softmax is 1, so o = v of the head's kv group."""
+    nq, nkv, hd = 32, 8, 128
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal(nq * hd).astype(np.float32)
+    k = rng.standard_normal((nkv, 16, hd)).astype(np.float16)
+    v = rng.standard_normal((nkv, 16, hd)).astype(np.float16)
+    o = ctx.attn_decode(ctx.to_device(q), ctx.to_device(k), ctx.to_device(v), nq, nkv, hd, 1, 16)
+    want = np.repeat(v[:, 0, :].astype(np.float32), nq // nkv, axis=0).reshape(-1)
+    np.testing.assert_array_equal(o, want)
+
+
+def test_attention_uniform_scores_is_mean(ctx):
+    """Closed form: identical K rows give uniform softmax weights, so o = mean over V rows."""
+    nq, nkv, hd, L = 8, 2, 64, 300
+    rng = np.random.default_rng(4)
+    q = rng.standard_normal(nq * hd).astype(np.float32)
+    k = np.repeat(rng.standard_normal((nkv, 1, hd)).astype(np.float16), 512, axis=1)
+    v = rng.standard_normal((nkv, 512, hd)).astype(np.float16)
+    o = ctx.attn_decode(ctx.to_device(q), ctx.to_device(k), ctx.to_device(v), nq, nkv, hd, L, 512)
+    want = np.repeat(v[:, :L, :].astype(np.float64).mean(axis=1), nq // nkv, axis=0).reshape(-1)
+    assert rel_l2(o, want) < 1e-6
+
+
+@pytest.mark.parametrize("n_chunks", [1, 3, 64, 256])
 def test_attention_chunking_invariant(ctx, n_chunks):
     nq, nkv, hd, L = 32, 8, 64, 700
     rng = np.random.default_rng(31)

@@ -176,15 +176,25 @@ int tpt_rope(tpt_ctx* c, float* x, int n_heads, int hd, int pos, const float* co
   return launch_rope(x, n_heads, hd, pos, cos_t, sin_t, c->stream);
 }
 
-int tpt_attn_decode(tpt_ctx* c, const float* q, const void* k_cache, const void* v_cache,
-                    float* o, int nq, int nkv, int hd, int L, int L_stride, int n_chunks) {
-  ENTER(c);
+namespace {
+// Shared set-up of the op-level attention entry points: argument checks and per-call scratch
+// (the chunk records of the split-K partition).
+struct AttnCall {
+  AttnArgs a;
+  void* scratch = nullptr;
+};
+int attn_prepare(tpt_ctx* c, const float* q, const void* k_cache, const void* v_cache,
+                 int kv_type, float* o, int nq, int nkv, int hd, int L, int L_stride,
+                 int n_chunks, AttnCall* call) {
   if (!q || !k_cache || !v_cache || !o) return fail(TPT_ERR_INVALID, "attention: null pointer");
   if (nkv <= 0 || nq <= 0 || nq % nkv) return fail(TPT_ERR_INVALID, "attention: bad head counts");
-  AttnArgs a;
+  if (L <= 0 || L > L_stride) return fail(TPT_ERR_INVALID, "attention: L must be in [1, L_stride]");
+  if (L > attn_max_len()) return fail(TPT_ERR_UNSUPPORTED, "attention: cache longer than the split-K partition supports");
+  AttnArgs& a = call->a;
   a.q = q;
-  a.kc = (const uint16_t*)k_cache;
-  a.vc = (const uint16_t*)v_cache;
+  a.kc = k_cache;
+  a.vc = v_cache;
+  a.kv_type = kv_type;
   a.o = o;
   a.nq = nq;
   a.nkv = nkv;
@@ -192,16 +202,47 @@ int tpt_attn_decode(tpt_ctx* c, const float* q, const void* k_cache, const void*
   a.L_stride = L_stride;
   a.L_host = L;
   a.n_chunks = n_chunks > 0 ? n_chunks : attn_default_chunks(L, nkv);
-  // per-call scratch: partial records and the per-kv-head arrival counters
   const size_t pf = (size_t)attn_part_floats(nq, nkv, hd, a.n_chunks);
-  void* scratch = nullptr;
-  TPT_HIP(hipMallocAsync(&scratch, pf * 4 + 256 + (size_t)nkv * 4, c->stream));
-  a.part = (float*)scratch;
-  a.counters = (unsigned int*)((char*)scratch + ((pf * 4 + 255) & ~(size_t)255));
-  hipError_t e = hipMemsetAsync(a.counters, 0, (size_t)nkv * 4, c->stream);
-  int rc = e == hipSuccess ? launch_attn_decode(a, c->stream) : hip_fail(e, "memset", __FILE__, __LINE__);
-  (void)hipFreeAsync(scratch, c->stream);
+  TPT_HIP(hipMallocAsync(&call->scratch, pf * 4, c->stream));
+  a.part = (float*)call->scratch;
+  return TPT_OK;
+}
+}  // namespace
+
+int tpt_attn_decode(tpt_ctx* c, const float* q, const void* k_cache, const void* v_cache,
+                    int kv_type, float* o, int nq, int nkv, int hd, int L, int L_stride,
+                    int n_chunks) {
+  ENTER(c);
+  AttnCall call;
+  int rc = attn_prepare(c, q, k_cache, v_cache, kv_type, o, nq, nkv, hd, L, L_stride, n_chunks, &call);
+  if (rc) return rc;
+  rc = launch_attn_decode(call.a, c->stream);
+  (void)hipFreeAsync(call.scratch, c->stream);
   return rc;
+}
+
+int tpt_bench_attn(tpt_ctx* c, const float* q, const void* k_cache, const void* v_cache,
+                   int kv_type, float* o, int nq, int nkv, int hd, int L, int L_stride,
+                   int n_chunks, int iters, float* ms_out) {
+  ENTER(c);
+  if (iters <= 0 || !ms_out) return fail(TPT_ERR_INVALID, "bench_attn: bad arguments");
+  AttnCall call;
+  int rc = attn_prepare(c, q, k_cache, v_cache, kv_type, o, nq, nkv, hd, L, L_stride, n_chunks, &call);
+  if (rc) return rc;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  hipError_t e = hipEventCreate(&e0);
+  if (e == hipSuccess) e = hipEventCreate(&e1);
+  if (e == hipSuccess) e = hipEventRecord(e0, c->stream);
+  for (int i = 0; i < iters && rc == TPT_OK && e == hipSuccess; i++) rc = launch_attn_decode(call.a, c->stream);
+  if (e == hipSuccess) e = hipEventRecord(e1, c->stream);
+  if (e == hipSuccess) e = hipEventSynchronize(e1);
+  if (e == hipSuccess && rc == TPT_OK) e = hipEventElapsedTime(ms_out, e0, e1);
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  (void)hipFreeAsync(call.scratch, c->stream);
+  if (rc) return rc;
+  if (e != hipSuccess) return hip_fail(e, "bench_attn", __FILE__, __LINE__);
+  return TPT_OK;
 }
 
 int tpt_argmax(tpt_ctx* c, const float* logits, int64_t n, uint32_t* out_host) {

@@ -32,6 +32,7 @@ struct tpt_engine {
   tpt_model* model = nullptr;
   tpt_model_info info{};
   std::vector<uint32_t> cached_tokens;  // tokens whose K/V occupy positions [0, n)
+  int kv_type = TPT_TYPE_F16;
 };
 
 namespace {
@@ -168,6 +169,14 @@ int tpt_engine_create(int device, tpt_engine** out) {
   return TPT_OK;
 }
 
+int tpt_engine_set_kv_type(tpt_engine* e, int kv_type) {
+  if (!e) return fail(TPT_ERR_INVALID, "null engine");
+  if (kv_type != TPT_TYPE_F16 && kv_type != TPT_TYPE_F32)
+    return fail(TPT_ERR_UNSUPPORTED, "KV cache type must be F16 or F32");
+  e->kv_type = kv_type;
+  return TPT_OK;
+}
+
 int tpt_engine_destroy(tpt_engine* e) {
   if (!e) return TPT_OK;
   tpt_engine_unload(e);
@@ -181,7 +190,7 @@ int tpt_engine_load(tpt_engine* e, const char* model_path, tpt_progress_fn progr
   if (!e || !model_path) return fail(TPT_ERR_INVALID, "null argument");
   tpt_engine_unload(e);  // free the previous model's HBM before allocating the next
   tpt_model* m = nullptr;
-  int rc = tpt_model_load(e->ctx, model_path, 0, progress, user, &m);
+  int rc = tpt_model_load(e->ctx, model_path, 0, e->kv_type, progress, user, &m);
   if (rc) return rc;
   e->model = m;
   e->cached_tokens.clear();

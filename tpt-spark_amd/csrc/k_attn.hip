@@ -1,4 +1,4 @@
-// Split-K (flash-decoding) GQA attention for one query position over an fp16 KV cache.
+// Split-K (flash-decoding) GQA attention for one query position over an fp16 or f32 KV cache.
 //
 // Replaces the three-pass attention.wgsl (src-tauri/src/engine/shaders/attention.wgsl:31-170,
 // dispatch_attention wgpu_engine.rs:666-726: scores materialised in f32 for every head and
@@ -6,14 +6,21 @@
 // CPU for a decode step: repeat_kv (head h reads kv head h / (Nq/Nkv)),
 // att = (q . k) * f32(1/sqrt(hd)), softmax_last_dim, att . v.
 //
-// Cache layout [Nkv][L_stride][hd] fp16 (one layer): the K and V rows of a kv head are
-// contiguous over positions, so a chunk of positions streams as one contiguous run.
-// Grid (n_chunks, Nkv), 256 threads.  A workgroup reads each K and V row of its chunk once
-// and serves all G = Nq/Nkv query heads of the group:
-//   phase 1: 16 lanes per position (hd/16 dims each) dot the G queries, scores -> LDS;
-//   phase 2: chunk max per head, p = exp(s - max), partial o = sum p*v and l = sum p;
-//   merge:   the last workgroup of a kv head (atomic counter) combines the chunks with the
-//            log-sum-exp rule and writes o; it also returns the counter to zero.
+// Cache layout [Nkv][L_stride][hd], element type fp16 (the default) or f32 (candle keeps an f32
+// cache): the K and V rows of a kv head are contiguous over positions, so a chunk of positions
+// streams as one contiguous run.  Two kernels:
+//  * attn_partial, grid (n_chunks, Nkv), 256 threads.  A workgroup reads each K and V row of its
+//    chunk once and serves all G = Nq/Nkv query heads of the group.  LPP lanes (16 B each)
+//    share a position and reduce with DPP; every thread keeps U rows in flight (loads are
+//    unconditional, positions past the chunk re-read its last row), and the first round's V
+//    rows are loaded together with its K rows (a chunk of up to R*U positions is one round
+//    trip).
+//    Scores go to LDS; after the chunk max, p = exp(s - max) is formed once per (head,
+//    position) and summed; then o = sum p v.  The record (o unnormalised, max, sum) goes to
+//    the partial buffer.
+//  * attn_merge, one workgroup per 32 output dims: combines the chunk records with the
+//    log-sum-exp rule; its first chunk loads are issued before the chunk weights are known.  The kernel boundary orders the two, so
+//    no device-wide fence or arrival counter is needed.
 #include "kernels.h"
 
 namespace tpt {
@@ -21,12 +28,19 @@ namespace {
 
 constexpr int ANT = 256;
 constexpr int ANW = ANT / WAVE;
-constexpr int CL_MAX = 1024;  // positions per chunk held in LDS
+constexpr int CL_MAX = 1024;   // positions per chunk held in LDS
+constexpr int NCH_MAX = 256;   // chunks per kv head
+constexpr int MT = 32;         // output dims per merge workgroup
+constexpr int MSETS = ANT / MT;
 
-template <int HD>
-__device__ __forceinline__ void load_half_slice(const uint16_t* p, float* out) {
-  constexpr int DPL = HD / 16;
-  if constexpr (DPL == 8) {
+// KV element traits: 16 bytes per lane per row => LPP lanes per position.
+template <typename T> struct KvTraits;
+template <> struct KvTraits<uint16_t> { static constexpr int LPP = 16; };
+template <> struct KvTraits<float> { static constexpr int LPP = 32; };
+
+template <int EPL>
+__device__ __forceinline__ void load_row(const uint16_t* p, float* out) {
+  if constexpr (EPL == 8) {
     const uint4 v = *(const uint4*)p;
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -34,7 +48,7 @@ __device__ __forceinline__ void load_half_slice(const uint16_t* p, float* out) {
       out[2 * i] = h2f((uint16_t)(w[i] & 0xffff));
       out[2 * i + 1] = h2f((uint16_t)(w[i] >> 16));
     }
-  } else if constexpr (DPL == 6) {
+  } else if constexpr (EPL == 6) {
     const uint32_t* q = (const uint32_t*)p;
     const uint32_t w[3] = {q[0], q[1], q[2]};
 #pragma unroll
@@ -43,7 +57,7 @@ __device__ __forceinline__ void load_half_slice(const uint16_t* p, float* out) {
       out[2 * i + 1] = h2f((uint16_t)(w[i] >> 16));
     }
   } else {
-    static_assert(DPL == 4, "head_dim must be 64, 96 or 128");
+    static_assert(EPL == 4, "fp16 rows: head_dim 64, 96 or 128");
     const uint2 v = *(const uint2*)p;
     const uint32_t w[2] = {v.x, v.y};
 #pragma unroll
@@ -54,50 +68,86 @@ __device__ __forceinline__ void load_half_slice(const uint16_t* p, float* out) {
   }
 }
 
-template <int HD, int G>
-__global__ void __launch_bounds__(ANT) attn_decode_kernel(const AttnArgs a, const float scale) {
-  constexpr int DPL = HD / 16;
-  constexpr int PSTRIDE = HD + 2;  // partial record: o[HD], m, l
-  __shared__ float s_sc[G][CL_MAX];
+template <int EPL>
+__device__ __forceinline__ void load_row(const float* p, float* out) {
+  if constexpr (EPL == 4) {
+    const float4 v = *(const float4*)p;
+    out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+  } else if constexpr (EPL == 3) {
+    out[0] = p[0]; out[1] = p[1]; out[2] = p[2];
+  } else {
+    static_assert(EPL == 2, "f32 rows: head_dim 64, 96 or 128");
+    const float2 v = *(const float2*)p;
+    out[0] = v.x; out[1] = v.y;
+  }
+}
+
+template <typename T, int HD, int G>
+__global__ void __launch_bounds__(ANT) attn_partial_kernel(const AttnArgs a, const float scale) {
+  constexpr int LPP = KvTraits<T>::LPP;   // lanes per position
+  constexpr int EPL = HD / LPP;           // elements per lane
+  constexpr int R = ANT / LPP;            // positions per round
+  constexpr int U = 8;                    // rounds whose loads are in flight together
+  constexpr int PSTRIDE = HD + 2;         // partial record: o[HD], m, l
+  __shared__ float s_p[G][CL_MAX];        // scores, then p = exp(s - max)
   __shared__ float s_red[ANW][G];
-  __shared__ float s_o[16][G][HD];
-  __shared__ float s_l[16][G];
-  __shared__ int s_last;
+  __shared__ float s_o[R][G][HD];
+  __shared__ float s_l[G];
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int li = lane & 15, pg = wid * 4 + (lane >> 4);  // position group 0..15
+  const int li = tid % LPP, pg = tid / LPP;  // lane in position, position group 0..R-1
   const int kvh = blockIdx.y, chunk = blockIdx.x, nch = gridDim.x;
   const int L = a.state ? a.state->pos + 1 : a.L_host;
   int CL = (L + nch - 1) / nch;
   CL = (CL + 15) & ~15;
-  if (CL > CL_MAX) CL = CL_MAX;  // the caller sizes n_chunks so that this never binds
+  if (CL > CL_MAX) CL = CL_MAX;  // the host sizes n_chunks so that this never binds
   const int p0 = chunk * CL;
   const int p1 = min(L, p0 + CL);
+  const int n = p1 - p0;  // may be <= 0 for trailing chunks
+  const int plast = p1 - 1;  // a valid row (p1 >= 1): target of the clamped loads
 
-  const uint16_t* K = a.kc + (size_t)kvh * a.L_stride * HD + li * DPL;
-  const uint16_t* V = a.vc + (size_t)kvh * a.L_stride * HD + li * DPL;
+  const T* K = (const T*)a.kc + (size_t)kvh * a.L_stride * HD + li * EPL;
+  const T* V = (const T*)a.vc + (size_t)kvh * a.L_stride * HD + li * EPL;
 
-  float q[G][DPL];
+  float q[G][EPL];
 #pragma unroll
   for (int h = 0; h < G; h++)
 #pragma unroll
-    for (int e = 0; e < DPL; e++) q[h][e] = a.q[(size_t)(kvh * G + h) * HD + li * DPL + e];
+    for (int e = 0; e < EPL; e++) q[h][e] = a.q[(size_t)(kvh * G + h) * HD + li * EPL + e];
 
-  // phase 1: scores
+  // phase 1: scores (the first round also fetches its V rows)
+  float vpre[U][EPL];
   float mloc[G];
 #pragma unroll
   for (int h = 0; h < G; h++) mloc[h] = -INFINITY;
-  for (int p = p0 + pg; p < p1; p += 16) {
-    float k[DPL];
-    load_half_slice<HD>(K + (size_t)p * HD, k);
+  for (int base = p0; base < p1; base += R * U) {
+    float k[U][EPL];
 #pragma unroll
-    for (int h = 0; h < G; h++) {
-      float s = 0.f;
+    for (int u = 0; u < U; u++) {
+      const int p = min(base + u * R + pg, plast);
+      load_row<EPL>(K + (size_t)p * HD, k[u]);
+    }
+    if (base == p0) {
 #pragma unroll
-      for (int e = 0; e < DPL; e++) s = fmaf(q[h][e], k[e], s);
-      s = group_sum<16>(s) * scale;
-      mloc[h] = fmaxf(mloc[h], s);
-      if (li == 0) s_sc[h][p - p0] = s;
+      for (int u = 0; u < U; u++) {
+        const int p = min(base + u * R + pg, plast);
+        load_row<EPL>(V + (size_t)p * HD, vpre[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int p = base + u * R + pg;
+#pragma unroll
+      for (int h = 0; h < G; h++) {
+        float s = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) s = fmaf(q[h][e], k[u][e], s);
+        s = lane_group_sum<LPP>(s) * scale;
+        if (p < p1) {
+          mloc[h] = fmaxf(mloc[h], s);
+          if (li == 0) s_p[h][p - p0] = s;
+        }
+      }
     }
   }
 #pragma unroll
@@ -113,32 +163,65 @@ __global__ void __launch_bounds__(ANT) attn_decode_kernel(const AttnArgs a, cons
 #pragma unroll
     for (int w = 1; w < ANW; w++) M[h] = fmaxf(M[h], s_red[w][h]);
   }
+  __syncthreads();  // s_red is reused below
 
-  // phase 2: p = exp(s - M), o = sum p v, l = sum p
-  float o[G][DPL], l[G];
+  // p = exp(s - M) once per (head, position); l = sum p
 #pragma unroll
   for (int h = 0; h < G; h++) {
-    l[h] = 0.f;
-#pragma unroll
-    for (int e = 0; e < DPL; e++) o[h][e] = 0.f;
+    float ls = 0.f;
+    for (int j = tid; j < n; j += ANT) {
+      const float w = expf(s_p[h][j] - M[h]);
+      s_p[h][j] = w;
+      ls += w;
+    }
+    ls = wave_sum(ls);
+    if (lane == 0) s_red[wid][h] = ls;
   }
-  for (int p = p0 + pg; p < p1; p += 16) {
-    float v[DPL];
-    load_half_slice<HD>(V + (size_t)p * HD, v);
+  __syncthreads();
+  if (tid < G) {
+    float t = 0.f;
 #pragma unroll
-    for (int h = 0; h < G; h++) {
-      const float w = expf(s_sc[h][p - p0] - M[h]);
-      l[h] += w;
+    for (int w = 0; w < ANW; w++) t += s_red[w][tid];
+    s_l[tid] = t;
+  }
+
+  // phase 2: o = sum p v
+  float o[G][EPL];
 #pragma unroll
-      for (int e = 0; e < DPL; e++) o[h][e] = fmaf(w, v[e], o[h][e]);
+  for (int h = 0; h < G; h++)
+#pragma unroll
+    for (int e = 0; e < EPL; e++) o[h][e] = 0.f;
+  for (int base = p0; base < p1; base += R * U) {
+    float vv[U][EPL];
+    if (base == p0) {
+#pragma unroll
+      for (int u = 0; u < U; u++)
+#pragma unroll
+        for (int e = 0; e < EPL; e++) vv[u][e] = vpre[u][e];
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const int p = min(base + u * R + pg, plast);
+        load_row<EPL>(V + (size_t)p * HD, vv[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int p = base + u * R + pg;
+      if (p < p1) {
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+          const float w = s_p[h][p - p0];
+#pragma unroll
+          for (int e = 0; e < EPL; e++) o[h][e] = fmaf(w, vv[u][e], o[h][e]);
+        }
+      }
     }
   }
 #pragma unroll
-  for (int h = 0; h < G; h++) {
+  for (int h = 0; h < G; h++)
 #pragma unroll
-    for (int e = 0; e < DPL; e++) s_o[pg][h][li * DPL + e] = o[h][e];
-    if (li == 0) s_l[pg][h] = l[h];
-  }
+    for (int e = 0; e < EPL; e++) s_o[pg][h][li * EPL + e] = o[h][e];
   __syncthreads();
 
   float* part = a.part + ((size_t)kvh * nch + chunk) * G * PSTRIDE;
@@ -146,62 +229,105 @@ __global__ void __launch_bounds__(ANT) attn_decode_kernel(const AttnArgs a, cons
     const int h = i / HD, d = i % HD;
     float s = 0.f;
 #pragma unroll
-    for (int g = 0; g < 16; g++) s += s_o[g][h][d];
+    for (int g = 0; g < R; g++) s += s_o[g][h][d];
     part[h * PSTRIDE + d] = s;
   }
   if (tid < G) {
-    float s = 0.f;
-#pragma unroll
-    for (int g = 0; g < 16; g++) s += s_l[g][tid];
-    part[tid * PSTRIDE + HD] = M[tid];
-    part[tid * PSTRIDE + HD + 1] = s;
+    part[tid * PSTRIDE + HD] = M[tid];  // -inf for an empty chunk (its l is 0)
+    part[tid * PSTRIDE + HD + 1] = s_l[tid];
   }
-
-  // merge: the last chunk of this kv head to finish combines all chunks
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) s_last = atomicAdd(&a.counters[kvh], 1u) == (unsigned)(nch - 1);
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  const float* pk = a.part + (size_t)kvh * nch * G * PSTRIDE;
-  // chunk weights exp(m_c - Mmax) per head, reusing s_sc as scratch [G][nch]
-  for (int h = wid; h < G; h += ANW) {
-    float mm = -INFINITY;
-    for (int c = lane; c < nch; c += WAVE) mm = fmaxf(mm, pk[((size_t)c * G + h) * PSTRIDE + HD]);
-    mm = wave_max(mm);
-    float ssum = 0.f;
-    for (int c = lane; c < nch; c += WAVE) {
-      const float* rec = pk + ((size_t)c * G + h) * PSTRIDE;
-      const float w = expf(rec[HD] - mm);
-      s_sc[h][c] = w;
-      ssum = fmaf(w, rec[HD + 1], ssum);
-    }
-    ssum = wave_sum(ssum);
-    if (lane == 0) s_red[0][h] = ssum;
-  }
-  __syncthreads();
-  for (int i = tid; i < G * HD; i += ANT) {
-    const int h = i / HD, d = i % HD;
-    float s = 0.f;
-    for (int c = 0; c < nch; c++) s = fmaf(s_sc[h][c], pk[((size_t)c * G + h) * PSTRIDE + d], s);
-    a.o[(size_t)(kvh * G + h) * HD + d] = s / s_red[0][h];
-  }
-  if (tid == 0) a.counters[kvh] = 0u;
 }
 
-template <int HD>
-int launch_hd(const AttnArgs& a, float scale, hipStream_t s) {
-  const dim3 grid((unsigned)a.n_chunks, (unsigned)a.nkv);
-  switch (a.nq / a.nkv) {
-    case 1: hipLaunchKernelGGL((attn_decode_kernel<HD, 1>), grid, dim3(ANT), 0, s, a, scale); break;
-    case 2: hipLaunchKernelGGL((attn_decode_kernel<HD, 2>), grid, dim3(ANT), 0, s, a, scale); break;
-    case 4: hipLaunchKernelGGL((attn_decode_kernel<HD, 4>), grid, dim3(ANT), 0, s, a, scale); break;
-    case 8: hipLaunchKernelGGL((attn_decode_kernel<HD, 8>), grid, dim3(ANT), 0, s, a, scale); break;
-    default: return fail(TPT_ERR_UNSUPPORTED, "attention: Nq/Nkv must be 1, 2, 4 or 8");
+// o[h][d] = sum_c w_c o_c[h][d] / sum_c w_c l_c with w_c = exp(m_c - max_c m_c).  Workgroup:
+// 32 consecutive output dims of one head; thread (set, j) sums chunks set, set + 8, ...
+template <int HD, int G>
+__global__ void __launch_bounds__(ANT) attn_merge_kernel(const float* __restrict__ part,
+                                                         float* __restrict__ out, int nch) {
+  constexpr int PSTRIDE = HD + 2;
+  constexpr int TILES = G * HD / MT;  // merge workgroups per kv head
+  __shared__ float s_w[NCH_MAX];
+  __shared__ float s_acc[MSETS][MT];
+  __shared__ float s_l;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int kvh = blockIdx.x / TILES, d0 = (blockIdx.x % TILES) * MT;
+  const int h = d0 / HD, dh = d0 % HD;
+  const float* pk = part + (size_t)kvh * nch * G * PSTRIDE + (size_t)h * PSTRIDE;
+  const int j = tid % MT, set = tid / MT;
+  const float* src = pk + dh + j;
+  // first 8 chunks of this thread's set, issued before the weights (clamped: always in bounds)
+  float v0[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) v0[i] = src[(size_t)min(set + i * MSETS, nch - 1) * G * PSTRIDE];
+  if (tid < WAVE) {
+    float mm = -INFINITY;
+    for (int c = lane; c < nch; c += WAVE) mm = fmaxf(mm, pk[(size_t)c * G * PSTRIDE + HD]);
+    mm = wave_max(mm);
+    float ls = 0.f;
+    for (int c = lane; c < nch; c += WAVE) {
+      const float* rec = pk + (size_t)c * G * PSTRIDE;
+      const float w = expf(rec[HD] - mm);
+      s_w[c] = w;
+      ls = fmaf(w, rec[HD + 1], ls);
+    }
+    ls = wave_sum(ls);
+    if (lane == 0) s_l = ls;
   }
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const int c = set + i * MSETS;
+    if (c < nch) s = fmaf(s_w[c], v0[i], s);
+  }
+  int c = set + 8 * MSETS;
+  for (; c + 7 * MSETS < nch; c += 8 * MSETS) {
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = src[(size_t)(c + i * MSETS) * G * PSTRIDE];
+#pragma unroll
+    for (int i = 0; i < 8; i++) s = fmaf(s_w[c + i * MSETS], v[i], s);
+  }
+  for (; c < nch; c += MSETS) s = fmaf(s_w[c], src[(size_t)c * G * PSTRIDE], s);
+  s_acc[set][j] = s;
+  __syncthreads();
+  if (tid < MT) {
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < MSETS; i++) t += s_acc[i][tid];
+    out[(size_t)(kvh * G + h) * HD + dh + tid] = t / s_l;
+  }
+}
+
+template <typename T, int HD, int G>
+int launch_g(const AttnArgs& a, float scale, hipStream_t s) {
+  hipLaunchKernelGGL((attn_partial_kernel<T, HD, G>), dim3((unsigned)a.n_chunks, (unsigned)a.nkv),
+                     dim3(ANT), 0, s, a, scale);
+  TPT_HIP(hipGetLastError());
+  hipLaunchKernelGGL((attn_merge_kernel<HD, G>), dim3((unsigned)(a.nkv * G * HD / MT)), dim3(ANT), 0,
+                     s, (const float*)a.part, a.o, a.n_chunks);
   TPT_HIP(hipGetLastError());
   return TPT_OK;
+}
+
+template <typename T, int HD>
+int launch_hd(const AttnArgs& a, float scale, hipStream_t s) {
+  switch (a.nq / a.nkv) {
+    case 1: return launch_g<T, HD, 1>(a, scale, s);
+    case 2: return launch_g<T, HD, 2>(a, scale, s);
+    case 4: return launch_g<T, HD, 4>(a, scale, s);
+    case 8: return launch_g<T, HD, 8>(a, scale, s);
+  }
+  return fail(TPT_ERR_UNSUPPORTED, "attention: Nq/Nkv must be 1, 2, 4 or 8");
+}
+
+template <typename T>
+int launch_t(const AttnArgs& a, float scale, hipStream_t s) {
+  switch (a.hd) {
+    case 64: return launch_hd<T, 64>(a, scale, s);
+    case 96: return launch_hd<T, 96>(a, scale, s);
+    case 128: return launch_hd<T, 128>(a, scale, s);
+  }
+  return fail(TPT_ERR_UNSUPPORTED, "attention: head_dim must be 64, 96 or 128");
 }
 
 }  // namespace
@@ -210,30 +336,33 @@ int attn_part_floats(int nq, int nkv, int hd, int n_chunks) {
   return nkv * n_chunks * (nq / nkv) * (hd + 2);
 }
 
+// Chunks per kv head: about 128 positions per workgroup (one round of loads for an fp16
+// cache) while the grid is small, at most 512 workgroups in total, and never more than CL_MAX
+// positions per chunk.
 int attn_default_chunks(int L, int nkv) {
-  int n = (L + 63) / 64;
-  const int cap = 1024 / (nkv > 0 ? nkv : 1);
+  int n = (L + 127) / 128;
+  int cap = 512 / (nkv > 0 ? nkv : 1);
+  if (cap < 1) cap = 1;
   if (n > cap) n = cap;
   const int need = (L + CL_MAX - 1) / CL_MAX;
   if (n < need) n = need;
+  if (n > NCH_MAX) n = NCH_MAX;
   return n < 1 ? 1 : n;
 }
 
+int attn_max_len() { return CL_MAX * NCH_MAX; }
+
 int launch_attn_decode(const AttnArgs& a, hipStream_t s) {
   if (a.nq <= 0 || a.nkv <= 0 || a.nq % a.nkv) return fail(TPT_ERR_INVALID, "attention: bad head counts");
-  if (a.n_chunks <= 0 || a.n_chunks > 4096) return fail(TPT_ERR_INVALID, "attention: bad chunk count");
+  if (a.n_chunks <= 0 || a.n_chunks > NCH_MAX) return fail(TPT_ERR_INVALID, "attention: chunk count must be in [1, 256]");
   if (!a.state && (a.L_host <= 0 || a.L_host > a.L_stride))
     return fail(TPT_ERR_INVALID, "attention: L must be in [1, L_stride]");
   if (!a.state && (a.L_host + a.n_chunks - 1) / a.n_chunks > CL_MAX)
     return fail(TPT_ERR_INVALID, "attention: too few chunks for this length");
-  if (a.n_chunks > CL_MAX) return fail(TPT_ERR_INVALID, "attention: too many chunks");
+  if (a.kv_type != TPT_TYPE_F16 && a.kv_type != TPT_TYPE_F32)
+    return fail(TPT_ERR_UNSUPPORTED, "attention: KV cache type must be F16 or F32");
   const float scale = (float)(1.0 / __builtin_sqrt((double)a.hd));
-  switch (a.hd) {
-    case 64: return launch_hd<64>(a, scale, s);
-    case 96: return launch_hd<96>(a, scale, s);
-    case 128: return launch_hd<128>(a, scale, s);
-  }
-  return fail(TPT_ERR_UNSUPPORTED, "attention: head_dim must be 64, 96 or 128");
+  return a.kv_type == TPT_TYPE_F32 ? launch_t<float>(a, scale, s) : launch_t<uint16_t>(a, scale, s);
 }
 
 }  // namespace tpt

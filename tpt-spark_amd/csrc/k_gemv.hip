@@ -513,11 +513,18 @@ __global__ void __launch_bounds__(NT) gemv_q8_kernel(const GemvArgs A) {
               const float cs = ein0[r], sn = ein1[r];
               // candle rope_i: dst[2i] = x0*cos - x1*sin; dst[2i+1] = x0*sin + x1*cos
               const float out = first ? (x0 * cs - x1 * sn) : (x0 * sn + x1 * cs);
-              if (isq) A.y[rr] = out;
-              else A.kcache[((size_t)(rr / A.hd) * A.max_ctx + pos) * A.hd + rr % A.hd] = f2h(out);
+              if (isq) {
+                A.y[rr] = out;
+              } else {
+                const size_t ci = ((size_t)(rr / A.hd) * A.max_ctx + pos) * A.hd + rr % A.hd;
+                if (A.kv_type == TPT_TYPE_F32) ((float*)A.kcache)[ci] = out;
+                else ((uint16_t*)A.kcache)[ci] = f2h(out);
+              }
             } else {
               const int rr = lrow - A.qd - A.kd;
-              A.vcache[((size_t)(rr / A.hd) * A.max_ctx + pos) * A.hd + rr % A.hd] = f2h(self);
+              const size_t ci = ((size_t)(rr / A.hd) * A.max_ctx + pos) * A.hd + rr % A.hd;
+              if (A.kv_type == TPT_TYPE_F32) ((float*)A.vcache)[ci] = self;
+              else ((uint16_t*)A.vcache)[ci] = f2h(self);
             }
           }
         } break;

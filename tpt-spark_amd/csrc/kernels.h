@@ -41,8 +41,9 @@ struct GemvArgs {
   int qd = 0, kd = 0, hd = 0, max_ctx = 0;
   const float* rope_cos = nullptr;
   const float* rope_sin = nullptr;
-  uint16_t* kcache = nullptr;
-  uint16_t* vcache = nullptr;
+  void* kcache = nullptr;        // [nkv][max_ctx][hd] of kv_type
+  void* vcache = nullptr;
+  int kv_type = TPT_TYPE_F16;    // TPT_TYPE_F16 or TPT_TYPE_F32
   const StepState* state = nullptr;  // position/parity source (nullptr: pos_host / slot 0)
   int pos_host = 0;
   // EPI_ARGMAX
@@ -63,18 +64,19 @@ int launch_argmax(const float* logits, int64_t n, unsigned long long* slot, hipS
 
 struct AttnArgs {
   const float* q = nullptr;
-  const uint16_t* kc = nullptr;  // [nkv][L_stride][hd]
-  const uint16_t* vc = nullptr;
+  const void* kc = nullptr;      // [nkv][L_stride][hd] of kv_type
+  const void* vc = nullptr;
+  int kv_type = TPT_TYPE_F16;    // TPT_TYPE_F16 or TPT_TYPE_F32
   float* o = nullptr;
   int nq = 0, nkv = 0, hd = 0, L_stride = 0;
   int L_host = 0;                    // used when state == nullptr
   const StepState* state = nullptr;  // L = state->pos + 1
   int n_chunks = 0;
-  float* part = nullptr;             // [nkv][n_chunks][G][hd + 2]
-  unsigned int* counters = nullptr;  // [nkv], zero on entry, left zero on exit
+  float* part = nullptr;             // [nkv][n_chunks][G][hd + 2] chunk records
 };
 int attn_part_floats(int nq, int nkv, int hd, int n_chunks);
 int attn_default_chunks(int L, int nkv);
+int attn_max_len();  // longest cache the split-K partition supports
 int launch_attn_decode(const AttnArgs& a, hipStream_t s);
 
 // Start of a decode step: pick the token, embed it (x = dequant(token_embd[tok])), advance the

@@ -53,8 +53,10 @@ tpt_model::~tpt_model() {
   if (ids_host) (void)hipHostFree(ids_host);
 }
 
-int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, tpt_progress_fn progress,
-                    void* user) {
+int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_type,
+                    tpt_progress_fn progress, void* user) {
+  if (kv_type != TPT_TYPE_F16 && kv_type != TPT_TYPE_F32)
+    return fail(TPT_ERR_UNSUPPORTED, "KV cache type must be F16 or F32");
   ctx = c;
   stream = c->stream;
   path = gguf_path;
@@ -238,22 +240,24 @@ int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, tpt_prog
   // ---- runtime state
   const int max_ctx = max_ctx_req > 0 ? max_ctx_req : desc.context_length;
   if (max_ctx <= 0) return fail(TPT_ERR_INVALID, "max_ctx must be positive");
+  if (max_ctx > attn_max_len()) return fail(TPT_ERR_UNSUPPORTED, "max_ctx exceeds the attention partition limit");
   desc.max_ctx = max_ctx;
+  desc.kv_type = kv_type;
+  kv_elem = kv_type == TPT_TYPE_F32 ? 4 : 2;
   attn_max_chunks = attn_default_chunks(max_ctx, nkv);
   for (int b = 64; b < max_ctx * 2; b *= 2) attn_max_chunks = std::max(attn_max_chunks, attn_default_chunks(b, nkv));
   const size_t kv_elems = (size_t)desc.n_layers * 2 * nkv * (size_t)max_ctx * hd;
   size_t ro = 0;
   auto carve = [&](size_t bytes) { size_t o = ro; ro = align_up(ro + bytes, 256); return o; };
-  const size_t o_kv = carve(kv_elems * 2), o_x = carve((size_t)H * 4), o_q = carve((size_t)qd * 4),
+  const size_t o_kv = carve(kv_elems * kv_elem), o_x = carve((size_t)H * 4), o_q = carve((size_t)qd * 4),
                o_at = carve((size_t)qd * 4), o_h = carve((size_t)desc.ffn * 4),
                o_lg = carve((size_t)desc.vocab * 4), o_rc = carve((size_t)max_ctx * hd / 2 * 4),
                o_rs = carve((size_t)max_ctx * hd / 2 * 4), o_st = carve(sizeof(StepState)),
                o_pr = carve((size_t)max_ctx * 4), o_tl = carve((size_t)max_ctx * 4),
-               o_ap = carve((size_t)attn_part_floats(nq, nkv, hd, attn_max_chunks) * 4),
-               o_ac = carve((size_t)nkv * 4);
+               o_ap = carve((size_t)attn_part_floats(nq, nkv, hd, attn_max_chunks) * 4);
   TPT_HIP(hipMalloc(&runtime, ro));
   uint8_t* R = (uint8_t*)runtime;
-  kv = (uint16_t*)(R + o_kv);
+  kv = R + o_kv;
   x = (float*)(R + o_x);
   qbuf = (float*)(R + o_q);
   attn = (float*)(R + o_at);
@@ -265,7 +269,6 @@ int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, tpt_prog
   prompt_dev = (uint32_t*)(R + o_pr);
   tok_log = (uint32_t*)(R + o_tl);
   attn_part = (float*)(R + o_ap);
-  attn_cnt = (unsigned int*)(R + o_ac);
   TPT_HIP(hipMemsetAsync(runtime, 0, ro, stream));  // load time, outside any graph
 
   // RoPE tables exactly as quantized_llama::precomput_freqs_cis: f32 theta = 1/base^(2i/d)
@@ -305,8 +308,8 @@ int tpt_model::enqueue_step(int n_chunks, bool lm_head) {
   const size_t layer_kv = (size_t)2 * nkv * mc * hd;
   for (int l = 0; l < desc.n_layers; l++) {
     const Layer& L = layers[l];
-    uint16_t* kc = kv + (size_t)l * layer_kv;
-    uint16_t* vc = kc + (size_t)nkv * mc * hd;
+    uint8_t* kc = (uint8_t*)kv + (size_t)l * layer_kv * kv_elem;
+    uint8_t* vc = kc + (size_t)nkv * mc * hd * kv_elem;
     // norm -> Q|K|V GEMV -> RoPE -> q buffer / fp16 KV append at state->pos
     GemvArgs g;
     g.K = H;
@@ -324,6 +327,7 @@ int tpt_model::enqueue_step(int n_chunks, bool lm_head) {
     g.rope_sin = rope_sin;
     g.kcache = kc;
     g.vcache = vc;
+    g.kv_type = desc.kv_type;
     g.state = st;
     if (L.qkv_adjacent) {
       g.w0 = L.q;
@@ -346,6 +350,7 @@ int tpt_model::enqueue_step(int n_chunks, bool lm_head) {
     at.q = qbuf;
     at.kc = kc;
     at.vc = vc;
+    at.kv_type = desc.kv_type;
     at.o = attn;
     at.nq = nq;
     at.nkv = nkv;
@@ -354,7 +359,6 @@ int tpt_model::enqueue_step(int n_chunks, bool lm_head) {
     at.state = st;
     at.n_chunks = n_chunks;
     at.part = attn_part;
-    at.counters = attn_cnt;
     if ((rc = launch_attn_decode(at, stream))) return rc;
     // x += Wo . attn
     GemvArgs wo;
@@ -557,13 +561,13 @@ int tpt_model::decode_greedy(uint32_t first, int pos0, int n_steps, int64_t stop
 
 extern "C" {
 
-int tpt_model_load(tpt_ctx* c, const char* gguf_path, int max_ctx, tpt_progress_fn progress,
-                   void* user, tpt_model** out) {
+int tpt_model_load(tpt_ctx* c, const char* gguf_path, int max_ctx, int kv_type,
+                   tpt_progress_fn progress, void* user, tpt_model** out) {
   int rc = ctx_enter(c);
   if (rc) return rc;
   if (!gguf_path || !out) return fail(TPT_ERR_INVALID, "null argument");
   tpt_model* m = new tpt_model();
-  rc = m->load(c, gguf_path, max_ctx, progress, user);
+  rc = m->load(c, gguf_path, max_ctx, kv_type, progress, user);
   if (rc) {
     delete m;
     return rc;

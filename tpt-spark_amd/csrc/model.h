@@ -33,14 +33,14 @@ struct tpt_model {
   const float* out_norm = nullptr;
 
   // runtime buffers
-  uint16_t* kv = nullptr;  // [layer][K|V][nkv][max_ctx][hd] fp16
+  void* kv = nullptr;  // [layer][K|V][nkv][max_ctx][hd] of desc.kv_type (fp16 or f32)
+  size_t kv_elem = 2;
   float *x = nullptr, *qbuf = nullptr, *attn = nullptr, *hbuf = nullptr, *logits = nullptr;
   float *rope_cos = nullptr, *rope_sin = nullptr;  // [max_ctx][hd/2]
   tpt::StepState* st = nullptr;
   uint32_t* prompt_dev = nullptr;  // [max_ctx] token ids by position
   uint32_t* tok_log = nullptr;     // [max_ctx] token consumed at each position
   float* attn_part = nullptr;
-  unsigned int* attn_cnt = nullptr;
   int attn_max_chunks = 0;
   void* runtime = nullptr;  // one allocation holding the buffers above
 
@@ -50,7 +50,8 @@ struct tpt_model {
   std::map<int, hipGraphExec_t> graphs;  // by attention chunk count
 
   ~tpt_model();
-  int load(tpt_ctx* c, const char* gguf_path, int max_ctx, tpt_progress_fn progress, void* user);
+  int load(tpt_ctx* c, const char* gguf_path, int max_ctx, int kv_type, tpt_progress_fn progress,
+           void* user);
   int enqueue_step(int n_chunks, bool lm_head);
   int launch_step(int L, bool lm_head);  // graph replay (or direct launches)
   int chunks_for(int L) const;

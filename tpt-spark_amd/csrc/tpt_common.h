@@ -66,6 +66,29 @@ __device__ __forceinline__ float group_sum(float v) {  // sum over aligned group
   for (int o = W / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, WAVE);
   return v;
 }
+// Sum over aligned groups of 16 lanes with DPP (no LDS traffic): quad_perm [1,0,3,2],
+// quad_perm [2,3,0,1], row_half_mirror, row_mirror.  Every lane of a group ends with the same
+// bits (each step adds a value to its partner's, and f32 addition is commutative).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               0xF, 0xF, false));
+}
+__device__ __forceinline__ float sum16(float v) {
+  v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_mov<0x141>(v);  // row_half_mirror: lane i <- lane 7-i within 8
+  v += dpp_mov<0x140>(v);  // row_mirror: lane i <- lane 15-i within 16
+  return v;
+}
+template <int W>
+__device__ __forceinline__ float lane_group_sum(float v) {  // aligned groups of W lanes
+  static_assert(W == 16 || W == 32 || W == 64, "group of 16, 32 or 64 lanes");
+  v = sum16(v);
+  if constexpr (W >= 32) v += __shfl_xor(v, 16, WAVE);
+  if constexpr (W >= 64) v += __shfl_xor(v, 32, WAVE);
+  return v;
+}
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));

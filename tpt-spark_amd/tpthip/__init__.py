@@ -35,7 +35,7 @@ TOKEN_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_uint32, C.c_int)
 class ModelDesc(C.Structure):
     _fields_ = [("architecture", C.c_char * 32)] + \
         [(n, C.c_int) for n in ("n_layers", "n_heads", "n_kv_heads", "head_dim", "embed", "ffn",
-                                "vocab", "context_length", "max_ctx")] + \
+                                "vocab", "context_length", "max_ctx", "kv_type")] + \
         [("rms_eps", C.c_float), ("rope_base", C.c_float), ("rope_scale", C.c_float),
          ("weight_bytes", C.c_uint64), ("decode_bytes_per_token", C.c_uint64)] + \
         [(n, C.c_int) for n in ("type_q", "type_k", "type_v", "type_o", "type_gate", "type_up",
@@ -75,9 +75,9 @@ EXPORTS = {
     "tpt_gemv_rmsnorm": ([P, I32, P, P, P, F32, P, I32, I32], I32),
     "tpt_rmsnorm": ([P, P, P, P, I32, F32], I32),
     "tpt_rope": ([P, P, I32, I32, I32, P, P], I32),
-    "tpt_attn_decode": ([P, P, P, P, P, I32, I32, I32, I32, I32, I32], I32),
+    "tpt_attn_decode": ([P, P, P, P, I32, P, I32, I32, I32, I32, I32, I32], I32),
     "tpt_argmax": ([P, P, I64, P], I32),
-    "tpt_model_load": ([P, C.c_char_p, I32, PROGRESS_FN, P, P], I32),
+    "tpt_model_load": ([P, C.c_char_p, I32, I32, PROGRESS_FN, P, P], I32),
     "tpt_model_describe": ([P, P], I32),
     "tpt_model_destroy": ([P], I32),
     "tpt_model_prefill": ([P, P, I32, I32, P, P], I32),
@@ -85,6 +85,7 @@ EXPORTS = {
     "tpt_model_decode_greedy": ([P, U32, I32, I32, I64, P], I32),
     "tpt_model_hidden": ([P, P], I32),
     "tpt_engine_create": ([I32, P], I32),
+    "tpt_engine_set_kv_type": ([P, I32], I32),
     "tpt_engine_destroy": ([P], I32),
     "tpt_engine_load": ([P, C.c_char_p, PROGRESS_FN, P, P], I32),
     "tpt_engine_unload": ([P], I32),
@@ -95,6 +96,7 @@ EXPORTS = {
     "tpt_engine_reset_cache": ([P], I32),
     "tpt_common_prefix_len": ([P, SZ, P, SZ], SZ),
     "tpt_bench_gemv": ([P, I32, P, I32, P, P, I32, I32, I32, P], I32),
+    "tpt_bench_attn": ([P, P, P, P, I32, P, I32, I32, I32, I32, I32, I32, I32, P], I32),
     "tpt_bench_copy": ([P, P, P, SZ, I32, P], I32),
 }
 
@@ -232,11 +234,20 @@ class Context:
         check(lib().tpt_rope(self.h, xbuf.ptr, n_heads, hd, pos, cosbuf.ptr, sinbuf.ptr))
         return xbuf.download(np.float32, n_heads * hd)
 
-    def attn_decode(self, qbuf, kbuf, vbuf, nq, nkv, hd, L, L_stride, n_chunks=0):
+    def attn_decode(self, qbuf, kbuf, vbuf, nq, nkv, hd, L, L_stride, n_chunks=0,
+                    kv_type=TYPE_F16):
         o = self.alloc(nq * hd * 4)
-        check(lib().tpt_attn_decode(self.h, qbuf.ptr, kbuf.ptr, vbuf.ptr, o.ptr, nq, nkv, hd, L,
-                                    L_stride, n_chunks))
+        check(lib().tpt_attn_decode(self.h, qbuf.ptr, kbuf.ptr, vbuf.ptr, kv_type, o.ptr, nq, nkv,
+                                    hd, L, L_stride, n_chunks))
         return o.download(np.float32, nq * hd)
+
+    def bench_attn(self, qbuf, kbuf, vbuf, obuf, nq, nkv, hd, L, L_stride, iters, n_chunks=0,
+                   kv_type=TYPE_F16):
+        """Event-timed back-to-back decode-attention launches over one cache; returns ms."""
+        ms = C.c_float()
+        check(lib().tpt_bench_attn(self.h, qbuf.ptr, kbuf.ptr, vbuf.ptr, kv_type, obuf.ptr, nq, nkv,
+                                   hd, L, L_stride, n_chunks, iters, C.byref(ms)))
+        return ms.value
 
     def bench_gemv(self, qtype, wbufs, xbuf, ybuf, K, N, iters):
         """Event-timed back-to-back GEMV launches over rotating weight copies; returns ms."""
@@ -258,13 +269,14 @@ class Context:
 
 
 class Model:
-    """tpt_model: a GGUF resident in HBM with its fp16 KV cache."""
+    """tpt_model: a GGUF resident in HBM with its KV cache (fp16, or f32 like candle's)."""
 
-    def __init__(self, ctx, path, max_ctx=0, on_progress=None):
+    def __init__(self, ctx, path, max_ctx=0, on_progress=None, kv_type=TYPE_F16):
         self.ctx = ctx
         self._cb = PROGRESS_FN(lambda u, d, t: on_progress(d, t)) if on_progress else PROGRESS_FN()
         h = C.c_void_p()
-        check(lib().tpt_model_load(ctx.h, path.encode(), max_ctx, self._cb, None, C.byref(h)))
+        check(lib().tpt_model_load(ctx.h, path.encode(), max_ctx, kv_type, self._cb, None,
+                                   C.byref(h)))
         self.h = h.value
         d = ModelDesc()
         check(lib().tpt_model_describe(self.h, C.byref(d)))
@@ -352,10 +364,12 @@ class HipEngine:
     """engine-hip behind the LlmEngine interface: load / unload / is_loaded / model_info /
     infer.  `detokenize(id) -> str` fills TokenEvent.token (default: the decimal id)."""
 
-    def __init__(self, device=0, detokenize: Optional[Callable[[int], str]] = None):
+    def __init__(self, device=0, detokenize: Optional[Callable[[int], str]] = None,
+                 kv_type=TYPE_F16):
         h = C.c_void_p()
         check(lib().tpt_engine_create(device, C.byref(h)))
         self.h = h.value
+        check(lib().tpt_engine_set_kv_type(self.h, kv_type))
         self.detokenize = detokenize or (lambda i: str(i))
         self.last_stats = None
 
