@@ -202,6 +202,7 @@ int attn_prepare(tpt_ctx* c, const float* q, const void* k_cache, const void* v_
   a.L_stride = L_stride;
   a.L_host = L;
   a.n_chunks = n_chunks > 0 ? n_chunks : attn_default_chunks(L, nkv);
+  a.chunk_len = attn_chunk_len(L, a.n_chunks);
   const size_t pf = (size_t)attn_part_floats(nq, nkv, hd, a.n_chunks);
   TPT_HIP(hipMallocAsync(&call->scratch, pf * 4, c->stream));
   a.part = (float*)call->scratch;

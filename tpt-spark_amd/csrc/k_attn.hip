@@ -82,12 +82,12 @@ __device__ __forceinline__ void load_row(const float* p, float* out) {
   }
 }
 
-template <typename T, int HD, int G>
+template <typename T, int HD, int G, int U>
 __global__ void __launch_bounds__(ANT) attn_partial_kernel(const AttnArgs a, const float scale) {
   constexpr int LPP = KvTraits<T>::LPP;   // lanes per position
   constexpr int EPL = HD / LPP;           // elements per lane
   constexpr int R = ANT / LPP;            // positions per round
-  constexpr int U = 8;                    // rounds whose loads are in flight together
+  // U: rounds whose loads are in flight together (R*U >= the chunk length when it is short)
   constexpr int PSTRIDE = HD + 2;         // partial record: o[HD], m, l
   __shared__ float s_p[G][CL_MAX];        // scores, then p = exp(s - max)
   __shared__ float s_red[ANW][G];
@@ -97,14 +97,14 @@ __global__ void __launch_bounds__(ANT) attn_partial_kernel(const AttnArgs a, con
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int li = tid % LPP, pg = tid / LPP;  // lane in position, position group 0..R-1
   const int kvh = blockIdx.y, chunk = blockIdx.x, nch = gridDim.x;
-  const int L = a.state ? a.state->pos + 1 : a.L_host;
-  int CL = (L + nch - 1) / nch;
-  CL = (CL + 15) & ~15;
-  if (CL > CL_MAX) CL = CL_MAX;  // the host sizes n_chunks so that this never binds
+  // The chunk's rows are known at launch; the live length L (from the step state on the
+  // decode path) only masks, so the K/V loads do not wait for it.
+  const int CL = a.chunk_len;
   const int p0 = chunk * CL;
+  const int plast = min(p0 + CL, a.L_stride) - 1;  // clamped loads stay inside the cache
+  const int L = a.state ? a.state->pos + 1 : a.L_host;
   const int p1 = min(L, p0 + CL);
   const int n = p1 - p0;  // may be <= 0 for trailing chunks
-  const int plast = p1 - 1;  // a valid row (p1 >= 1): target of the clamped loads
 
   const T* K = (const T*)a.kc + (size_t)kvh * a.L_stride * HD + li * EPL;
   const T* V = (const T*)a.vc + (size_t)kvh * a.L_stride * HD + li * EPL;
@@ -120,7 +120,7 @@ __global__ void __launch_bounds__(ANT) attn_partial_kernel(const AttnArgs a, con
   float mloc[G];
 #pragma unroll
   for (int h = 0; h < G; h++) mloc[h] = -INFINITY;
-  for (int base = p0; base < p1; base += R * U) {
+  for (int base = p0; base < p0 + CL && base < L; base += R * U) {
     float k[U][EPL];
 #pragma unroll
     for (int u = 0; u < U; u++) {
@@ -300,8 +300,12 @@ __global__ void __launch_bounds__(ANT) attn_merge_kernel(const float* __restrict
 
 template <typename T, int HD, int G>
 int launch_g(const AttnArgs& a, float scale, hipStream_t s) {
-  hipLaunchKernelGGL((attn_partial_kernel<T, HD, G>), dim3((unsigned)a.n_chunks, (unsigned)a.nkv),
-                     dim3(ANT), 0, s, a, scale);
+  const dim3 grid((unsigned)a.n_chunks, (unsigned)a.nkv);
+  constexpr int R = ANT / KvTraits<T>::LPP;
+  if (a.chunk_len <= 4 * R)
+    hipLaunchKernelGGL((attn_partial_kernel<T, HD, G, 4>), grid, dim3(ANT), 0, s, a, scale);
+  else
+    hipLaunchKernelGGL((attn_partial_kernel<T, HD, G, 8>), grid, dim3(ANT), 0, s, a, scale);
   TPT_HIP(hipGetLastError());
   hipLaunchKernelGGL((attn_merge_kernel<HD, G>), dim3((unsigned)(a.nkv * G * HD / MT)), dim3(ANT), 0,
                      s, (const float*)a.part, a.o, a.n_chunks);
@@ -336,11 +340,10 @@ int attn_part_floats(int nq, int nkv, int hd, int n_chunks) {
   return nkv * n_chunks * (nq / nkv) * (hd + 2);
 }
 
-// Chunks per kv head: about 128 positions per workgroup (one round of loads for an fp16
-// cache) while the grid is small, at most 512 workgroups in total, and never more than CL_MAX
-// positions per chunk.
+// Chunks per kv head: about 64 positions per workgroup while the grid is small, at most 512
+// workgroups in total, and never more than CL_MAX positions per chunk.
 int attn_default_chunks(int L, int nkv) {
-  int n = (L + 127) / 128;
+  int n = (L + 63) / 64;
   int cap = 512 / (nkv > 0 ? nkv : 1);
   if (cap < 1) cap = 1;
   if (n > cap) n = cap;
@@ -352,13 +355,20 @@ int attn_default_chunks(int L, int nkv) {
 
 int attn_max_len() { return CL_MAX * NCH_MAX; }
 
+int attn_chunk_len(int L, int n_chunks) {
+  int cl = (L + n_chunks - 1) / n_chunks;
+  return (cl + 15) & ~15;
+}
+
 int launch_attn_decode(const AttnArgs& a, hipStream_t s) {
   if (a.nq <= 0 || a.nkv <= 0 || a.nq % a.nkv) return fail(TPT_ERR_INVALID, "attention: bad head counts");
   if (a.n_chunks <= 0 || a.n_chunks > NCH_MAX) return fail(TPT_ERR_INVALID, "attention: chunk count must be in [1, 256]");
   if (!a.state && (a.L_host <= 0 || a.L_host > a.L_stride))
     return fail(TPT_ERR_INVALID, "attention: L must be in [1, L_stride]");
-  if (!a.state && (a.L_host + a.n_chunks - 1) / a.n_chunks > CL_MAX)
-    return fail(TPT_ERR_INVALID, "attention: too few chunks for this length");
+  if (a.chunk_len <= 0 || a.chunk_len % 16 || a.chunk_len > CL_MAX)
+    return fail(TPT_ERR_INVALID, "attention: chunk length must be a multiple of 16 in [16, 1024]");
+  if (!a.state && (long)a.chunk_len * a.n_chunks < a.L_host)
+    return fail(TPT_ERR_INVALID, "attention: chunks do not cover the length");
   if (a.kv_type != TPT_TYPE_F16 && a.kv_type != TPT_TYPE_F32)
     return fail(TPT_ERR_UNSUPPORTED, "attention: KV cache type must be F16 or F32");
   const float scale = (float)(1.0 / __builtin_sqrt((double)a.hd));

@@ -7,22 +7,28 @@
 //   k_quants::matmul -> BlockQ8K::from_float (activation quant) -> vec_dot_q4k_q8k /
 //   vec_dot_q6k_q8k / vec_dot_q8_0_q8_0 (integer sums, f32 block scaling).
 //
-// Layout of the work (MI355X: 256 CUs, wave64, 160 KB LDS/CU, HBM3E):
-//  * A persistent grid of ~1 workgroup per CU (512 threads = 8 waves).  Each wave owns a
-//    contiguous range of rows, so a row's K/256 super-blocks stream as one contiguous run.
-//  * Prologue, once per workgroup: the activation (optionally RMS-normalised first) is
-//    quantized exactly like candle's CPU path into LDS: Q8_K (per 256: signed max-abs value,
-//    iscale = -128/max, round half away from zero, clamp 127, d = 1/iscale, per-16 sums) for
-//    k-quant weights, Q8_0 (per 32: d = amax/127 stored as f16, q = round(x/d)) for Q8_0.
-//    The weight loads of each wave's first rows are issued before it, so the prologue runs
+// Work layout (MI355X: 256 CUs, wave64, 160 KB LDS/CU, HBM3E):
+//  * A lane owns a "group" of 64 weights: a quarter of a k-quant super-block (Q4_K: 32 qs bytes
+//    + the block's 16-byte header; Q6_K: one (half, 16-column) slice: 2 x 16 ql bytes, 16 qh
+//    bytes, its 8 scales and d; Q8_0: two 34-byte blocks).  A "pass" covers BPP super-blocks
+//    of a row (4 lanes each); when a row has fewer than 16 super-blocks a pass covers
+//    RPP = 16/BPP rows, so every lane of the wave has work.
+//  * A wave runs RB rows in lockstep over a flattened sequence of (row group, pass) steps and
+//    double-buffers them: the loads of step s+1 are in flight while step s is computed.  Loads
+//    are unconditional (indices clamped into the matrix) so that the compiler never has to
+//    wait on them one by one.  Workgroups own contiguous row ranges; the waves of a workgroup
+//    split its row groups (and, for long rows, the passes: KS-way split of K).
+//  * Prologue, once per workgroup: x (optionally RMS-normalised) is quantized exactly like
+//    candle's CPU path into LDS -- Q8_K (per 256: signed max-abs value, iscale = -128/max,
+//    round half away from zero, clamp 127, d = 1/iscale, per-16 sums) for k-quant weights,
+//    Q8_0 (per 32: d = amax/127 rounded to f16, q = round(x/d)) for Q8_0 weights.  The x loads
+//    are issued first and the first step's weight loads right after, so the prologue runs
 //    under HBM latency.
-//  * Lanes: a "group" is 64 weights (Q4_K: 32 qs bytes of one super-block + its 16-byte
-//    header; Q6_K: one (pass, half) slice of a super-block; Q8_0: two blocks).  LPR lanes
-//    share a row, each lane owns GPL groups, and keeps its activation slice in registers for
-//    every row it visits.  Integer dots use v_dot4_i32_i8; each group ends in f32 block
-//    scaling; lanes reduce with cross-lane shuffles.
-//  * Epilogues fuse what follows the GEMV in run_forward_pass (wgpu_engine.rs:373-486):
-//    residual add, interleaved RoPE + fp16 KV-cache append, SiLU(gate)*up, greedy argmax.
+//  * Integer dots use v_dot4_i32_i8; each group ends in f32 block scaling (candle's per-block
+//    arithmetic), lanes accumulate in f32 and a row is reduced across its lanes once, with
+//    DPP.  Row results go to LDS, and after a workgroup barrier the epilogue stores them:
+//    plain, + residual, SiLU(gate)*up, interleaved RoPE + KV-cache append, or greedy argmax
+//    (what follows the GEMV in run_forward_pass, wgpu_engine.rs:373-486).
 #include "kernels.h"
 
 namespace tpt {
@@ -31,17 +37,18 @@ namespace {
 
 constexpr int NT = 512;  // threads per workgroup
 constexpr int NW = NT / WAVE;
-
-// ----------------------------------------------------------------- activation in registers
-struct Act {
-  int q[16];    // 64 int8 activation values of this lane's group, packed
-  float d0, d1; // Q8_K: d0 = block d;  Q8_0: d of each 32-block
-  int s[4];     // Q4_K: s[0], s[1] = sums over each 32;  Q6_K: per-16 sums of the 4 quads
-};
+constexpr int MAXB = 64 / NW;       // 256-element activation blocks per wave (K <= 16384)
 
 __device__ __forceinline__ uint32_t bsel(uint32_t v, int i) { return (v >> (8 * i)) & 0xffu; }
 
-// ----------------------------------------------------------------- raw weight slices
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+// ----------------------------------------------------------------- per-lane weight groups
+// group g of a row = 64 weights: Q4_K (block g/4, qs bytes 32(g%4)..), Q6_K (block g/4, half
+// (g/2)%2, column half g%2), Q8_0 (blocks 2g, 2g+1)
 template <int WT> struct Raw;
 template <> struct Raw<TPT_TYPE_Q4_K> { uint4 h, a, b; };
 template <> struct Raw<TPT_TYPE_Q6_K> { uint4 qa, qb, qh; uint2 sc; uint32_t d; };
@@ -63,7 +70,7 @@ __device__ __forceinline__ void load_raw<TPT_TYPE_Q4_K>(const uint8_t* row, int 
 template <>
 __device__ __forceinline__ void load_raw<TPT_TYPE_Q6_K>(const uint8_t* row, int g,
                                                          Raw<TPT_TYPE_Q6_K>& r) {
-  const uint8_t* blk = row + (size_t)(g >> 2) * 210;  // 2-byte aligned: unaligned loads
+  const uint8_t* blk = row + (size_t)(g >> 2) * 210;  // 2-byte aligned: unaligned vector loads
   const int p = (g >> 1) & 1, h = g & 1;
   r.qa = ldg_u<uint4>(blk + 64 * p + 16 * h);
   r.qb = ldg_u<uint4>(blk + 64 * p + 32 + 16 * h);
@@ -84,26 +91,230 @@ __device__ __forceinline__ void load_raw<TPT_TYPE_Q8_0>(const uint8_t* row, int 
   r.b1 = ldg_u<uint4>(b0 + 52);
 }
 
-// Q4_K x Q8_K for one group: restates vec_dot_q4k_q8k's per-block arithmetic
-// (d_w*d_x * sum_j sc_j * sum(q4*q8)  -  dmin_w*d_x * sum_j m_j * bsum_j).
-__device__ __forceinline__ float dot_group(const Raw<TPT_TYPE_Q4_K>& r, const Act& a, int g) {
-  const int g4 = g & 3;
-  // get_scale_min_k4 for j0 = 2*g4 and j1 = j0 + 1 (scales bytes: h.y = s[0..3],
-  // h.z = s[4..7], h.w = s[8..11])
-  int sc0, m0, sc1, m1;
-  if (g4 < 2) {
-    const int j0 = 2 * g4;
-    sc0 = bsel(r.h.y, j0) & 63;
-    m0 = bsel(r.h.z, j0) & 63;
-    sc1 = bsel(r.h.y, j0 + 1) & 63;
-    m1 = bsel(r.h.z, j0 + 1) & 63;
-  } else {
-    const int k = 2 * g4 - 4;
-    sc0 = (bsel(r.h.w, k) & 0xF) | ((bsel(r.h.y, k) >> 6) << 4);
-    m0 = (bsel(r.h.w, k) >> 4) | ((bsel(r.h.z, k) >> 6) << 4);
-    sc1 = (bsel(r.h.w, k + 1) & 0xF) | ((bsel(r.h.y, k + 1) >> 6) << 4);
-    m1 = (bsel(r.h.w, k + 1) >> 4) | ((bsel(r.h.z, k + 1) >> 6) << 4);
+// ----------------------------------------------------------------- activation (LDS)
+// LDS layout: qs int8[K] | d float[K/bs] | s16 int[K/16] | scratch float[NW] | rows
+struct Lds {
+  int* q32;
+  float* d;
+  int* s16;
+  float* red;
+  float* rows;
+};
+
+__host__ __device__ inline size_t lds_act_bytes(int K, bool q80) {
+  const int nd = q80 ? K / QK8_0 : K / QK_K;
+  return (size_t)K + 4 * nd + 4 * (K / 16) + 4 * NW;
+}
+
+__device__ __forceinline__ Lds lds_layout(char* smem, int K, bool q80) {
+  Lds l;
+  l.q32 = (int*)smem;
+  l.d = (float*)(smem + K);
+  const int nd = q80 ? K / QK8_0 : K / QK_K;
+  l.s16 = (int*)(smem + K + 4 * nd);
+  l.red = (float*)(smem + K + 4 * nd + 4 * (K / 16));
+  l.rows = l.red + NW;
+  return l;
+}
+
+__device__ __forceinline__ void barrier_lds() {
+  // LDS-only barrier: outstanding global loads (the prefetched weights) stay in flight.
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Activation preload: one float4 per lane per 256-element block, blocks b = wave, wave + NW,
+// ...  Loads are unconditional (clamped block index, x itself as a dummy norm source) so the
+// waitcnt pass can count exactly how many later loads may stay in flight.
+struct XPre {
+  float4 x[MAXB];
+  float4 w[MAXB];
+};
+
+__device__ __forceinline__ void preload_x(const GemvArgs& A, XPre& p) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int nb = A.K / 256;
+  const float4* xs = (const float4*)A.x;
+  const float4* ws = (const float4*)(A.prologue == PRO_RMSNORM ? A.norm_w : A.x);
+#pragma unroll
+  for (int i = 0; i < MAXB; i++) {
+    int b = wid + i * NW;
+    if (b >= nb) b = nb - 1;
+    p.x[i] = xs[b * 64 + lane];
+    p.w[i] = ws[b * 64 + lane];
   }
+}
+
+// 1/m of rms_norm (candle_nn::ops::rms_norm: m = sqrt(sum(x^2)/dim + eps)).  Every workgroup
+// reduces the whole vector itself from the preloaded registers (each element is owned by
+// exactly one lane of the workgroup).
+__device__ float rms_denominator(const GemvArgs& A, const XPre& p, float* red) {
+  const int tid = threadIdx.x, wid = tid >> 6;
+  const int nb = A.K / 256;
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXB; i++) {
+    if (wid + i * NW < nb) {
+      const float4 v = p.x[i];
+      ss = fmaf(v.x, v.x, ss);
+      ss = fmaf(v.y, v.y, ss);
+      ss = fmaf(v.z, v.z, ss);
+      ss = fmaf(v.w, v.w, ss);
+    }
+  }
+  ss = wave_sum_dpp(ss);
+  if ((tid & 63) == 0) red[wid] = ss;
+  barrier_lds();
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < NW; i++) t += red[i];
+  return sqrtf(t / (float)A.K + A.eps);
+}
+
+__device__ __forceinline__ float4 apply_norm(float4 v, float4 w, float m) {
+  v.x = v.x / m * w.x;
+  v.y = v.y / m * w.y;
+  v.z = v.z / m * w.z;
+  v.w = v.w / m * w.w;
+  return v;
+}
+
+// Q8_K quantization of one 256-block per wave (BlockQ8K::from_float).  The blocks of a wave
+// are independent, so their reductions interleave.
+__device__ void prologue_q8k(const GemvArgs& A, const XPre& p, const Lds& L) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int nb = A.K / QK_K;
+  float m = 1.f;
+  const bool norm = A.prologue == PRO_RMSNORM;
+  if (norm) m = rms_denominator(A, p, L.red);
+#pragma unroll
+  for (int i = 0; i < MAXB; i++) {
+    const int b = wid + i * NW;
+    if (b < nb) {
+      const float4 v = norm ? apply_norm(p.x[i], p.w[i], m) : p.x[i];
+      const float e[4] = {v.x, v.y, v.z, v.w};
+      // the signed value of largest |x|, first occurrence winning ties: the max of |x| over
+      // the wave, then the first lane (and its first element) holding it
+      const float la = fmaxf(fmaxf(fabsf(e[0]), fabsf(e[1])), fmaxf(fabsf(e[2]), fabsf(e[3])));
+      const float amax = wave_max_dpp(la);
+      const float mine = fabsf(e[0]) == amax ? e[0] : fabsf(e[1]) == amax ? e[1]
+                         : fabsf(e[2]) == amax ? e[2] : e[3];
+      const unsigned long long hit = __ballot(la == amax);
+      const int first = hit ? (int)__builtin_ctzll(hit) : 0;
+      const float mx = readlane_f(mine, first);
+      int packed = 0, qsum = 0;
+      float d = 0.f;
+      if (amax != 0.f) {
+        const float iscale = -128.f / mx;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          float r = roundf(iscale * e[j]);
+          r = fminf(r, 127.f);
+          r = fmaxf(r, -128.f);
+          const int q = (int)r;
+          qsum += q;
+          packed |= (q & 0xff) << (8 * j);
+        }
+        d = 1.f / iscale;
+      }
+      L.q32[b * 64 + lane] = packed;
+      qsum += dpp_i<0xB1>(qsum);  // sums of 16 values: groups of 4 lanes
+      qsum += dpp_i<0x4E>(qsum);
+      if ((lane & 3) == 0) L.s16[b * 16 + (lane >> 2)] = qsum;
+      if (lane == 0) L.d[b] = d;
+    }
+  }
+}
+
+// Q8_0 activation quantization (BlockQ8_0::from_float): 8 lanes per 32-block.
+__device__ void prologue_q80(const GemvArgs& A, const XPre& p, const Lds& L) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int nb = A.K / 256;
+  float m = 1.f;
+  const bool norm = A.prologue == PRO_RMSNORM;
+  if (norm) m = rms_denominator(A, p, L.red);
+#pragma unroll
+  for (int i = 0; i < MAXB; i++) {
+    const int c = wid + i * NW;
+    if (c < nb) {
+      const float4 v = norm ? apply_norm(p.x[i], p.w[i], m) : p.x[i];
+      float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+      amax = fmaxf(amax, dpp_mov<0xB1>(amax));   // max over 8 lanes
+      amax = fmaxf(amax, dpp_mov<0x4E>(amax));
+      amax = fmaxf(amax, dpp_mov<0x141>(amax));
+      const float d = amax / 127.f;
+      const float id = d != 0.f ? 1.f / d : 0.f;
+      const float e[4] = {v.x, v.y, v.z, v.w};
+      int packed = 0;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        float r = roundf(e[j] * id);
+        r = fminf(fmaxf(r, -128.f), 127.f);
+        packed |= ((int)r & 0xff) << (8 * j);
+      }
+      L.q32[c * 64 + lane] = packed;
+      if ((lane & 7) == 0) L.d[c * 8 + (lane >> 3)] = h2f(f2h(d));  // stored as f16
+    }
+  }
+}
+
+// ----------------------------------------------------------------- activation slices
+struct Act {
+  int q[16];     // the group's 64 int8 activation values, packed
+  float d0, d1;  // Q8_K: d0 = block d;  Q8_0: d of each 32-block
+  int s[4];      // Q4_K: s[0], s[1] = sums over each 32;  Q6_K: per-16 sums of the 4 quads
+};
+
+template <int WT>
+__device__ __forceinline__ void load_act(const Lds& L, int g, Act& a) {
+  if constexpr (WT == TPT_TYPE_Q4_K) {
+    const int4* q = (const int4*)(L.q32 + 16 * g);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int4 v = q[i];
+      a.q[4 * i] = v.x; a.q[4 * i + 1] = v.y; a.q[4 * i + 2] = v.z; a.q[4 * i + 3] = v.w;
+    }
+    a.d0 = L.d[g >> 2];
+    const int4 bs = *(const int4*)(L.s16 + 4 * g);
+    a.s[0] = bs.x + bs.y;
+    a.s[1] = bs.z + bs.w;
+  } else if constexpr (WT == TPT_TYPE_Q6_K) {
+    const int b = g >> 2, p = (g >> 1) & 1, h = g & 1;
+#pragma unroll
+    for (int quad = 0; quad < 4; quad++) {
+      const int4 v = *(const int4*)(L.q32 + (256 * b + 128 * p + 32 * quad + 16 * h) / 4);
+      a.q[4 * quad] = v.x; a.q[4 * quad + 1] = v.y; a.q[4 * quad + 2] = v.z; a.q[4 * quad + 3] = v.w;
+    }
+    const int4 s0 = *(const int4*)(L.s16 + 16 * b + 8 * p), s1 = *(const int4*)(L.s16 + 16 * b + 8 * p + 4);
+    // per-16 sums of elements 128p + 32quad + 16h: s16 index 8p + 2quad + h
+    a.s[0] = h ? s0.y : s0.x;
+    a.s[1] = h ? s0.w : s0.z;
+    a.s[2] = h ? s1.y : s1.x;
+    a.s[3] = h ? s1.w : s1.z;
+    a.d0 = L.d[b];
+  } else {
+    const int4* q = (const int4*)(L.q32 + 16 * g);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int4 v = q[i];
+      a.q[4 * i] = v.x; a.q[4 * i + 1] = v.y; a.q[4 * i + 2] = v.z; a.q[4 * i + 3] = v.w;
+    }
+    a.d0 = L.d[2 * g];
+    a.d1 = L.d[2 * g + 1];
+  }
+}
+
+// Q4_K x Q8_K for one group: vec_dot_q4k_q8k's per-block arithmetic restricted to the group's
+// two sub-blocks, d_w*d_x * sum_j sc_j * sum(q4*q8)  -  dmin_w*d_x * sum_j m_j * bsum_j.
+// get_scale_min_k4 for j0 = 2(g%4), j1 = j0 + 1 without branches: the scale bytes sit at byte
+// offset 2(g%2) of the header dwords y = s[0..3], z = s[4..7], w = s[8..11].
+__device__ __forceinline__ float dot_group(const Raw<TPT_TYPE_Q4_K>& r, const Act& a, int g) {
+  const int sh = 16 * (g & 1);
+  const uint32_t Y = r.h.y >> sh, Z = r.h.z >> sh, W = r.h.w >> sh;
+  const bool hi = (g & 2) != 0;
+  const int sc0 = hi ? (int)((W & 0xF) | (((Y >> 6) & 3) << 4)) : (int)(Y & 63);
+  const int sc1 = hi ? (int)(((W >> 8) & 0xF) | (((Y >> 14) & 3) << 4)) : (int)((Y >> 8) & 63);
+  const int m0 = hi ? (int)(((W >> 4) & 0xF) | (((Z >> 6) & 3) << 4)) : (int)(Z & 63);
+  const int m1 = hi ? (int)(((W >> 12) & 0xF) | (((Z >> 14) & 3) << 4)) : (int)((Z >> 8) & 63);
   const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
   int s0 = 0, s1 = 0;
 #pragma unroll
@@ -118,7 +329,7 @@ __device__ __forceinline__ float dot_group(const Raw<TPT_TYPE_Q4_K>& r, const Ac
   return dd * (float)isum - dm * (float)msum;
 }
 
-// Q6_K x Q8_K for one group (pass p, half h): vec_dot_q6k_q8k's per-block arithmetic,
+// Q6_K x Q8_K for one group (half p, column half h): vec_dot_q6k_q8k's per-block arithmetic,
 // d_w*d_x * sum_quad sc * (sum(q6*q8) - 32*bsum).
 __device__ __forceinline__ float dot_group(const Raw<TPT_TYPE_Q6_K>& r, const Act& a, int g) {
   const int h = g & 1;
@@ -138,9 +349,9 @@ __device__ __forceinline__ float dot_group(const Raw<TPT_TYPE_Q6_K>& r, const Ac
     d3 = sdot4((int)v3, a.q[12 + i], d3);
   }
   // scales of quads 0..3 are bytes h, h+2, h+4, h+6 of the 8 loaded (sc[8p .. 8p+8))
-  const uint32_t slo = r.sc.x, shi = r.sc.y;
-  const int sc0 = (int8_t)bsel(slo, h), sc1 = (int8_t)bsel(slo, h + 2);
-  const int sc2 = (int8_t)bsel(shi, h), sc3 = (int8_t)bsel(shi, h + 2);
+  const uint32_t slo = r.sc.x >> (8 * h), shi = r.sc.y >> (8 * h);
+  const int sc0 = (int8_t)(slo & 0xff), sc1 = (int8_t)((slo >> 16) & 0xff);
+  const int sc2 = (int8_t)(shi & 0xff), sc3 = (int8_t)((shi >> 16) & 0xff);
   const int isum = sc0 * (d0 - 32 * a.s[0]) + sc1 * (d1 - 32 * a.s[1]) +
                    sc2 * (d2 - 32 * a.s[2]) + sc3 * (d3 - 32 * a.s[3]);
   return (h2f((uint16_t)r.d) * a.d0) * (float)isum;
@@ -159,389 +370,202 @@ __device__ __forceinline__ float dot_group(const Raw<TPT_TYPE_Q8_0>& r, const Ac
   return ((float)s0 * h2f((uint16_t)r.d0)) * a.d0 + ((float)s1 * h2f((uint16_t)r.d1)) * a.d1;
 }
 
-// ----------------------------------------------------------------- prologue (LDS)
-// LDS layout: qs int8[K] | d float[K/bs] | s16 int[K/16] | scratch float[NW]
-struct Lds {
-  int* q32;
-  float* d;
-  int* s16;
-  float* red;
-};
-
-__device__ __forceinline__ Lds lds_layout(char* smem, int K, bool q80) {
-  Lds l;
-  l.q32 = (int*)smem;
-  l.d = (float*)(smem + K);
-  const int nd = q80 ? K / QK8_0 : K / QK_K;
-  l.s16 = (int*)(smem + K + 4 * nd);
-  l.red = (float*)(smem + K + 4 * nd + 4 * (K / 16));
-  return l;
-}
-
-__device__ __forceinline__ float eps_of(const GemvArgs& A) { return A.eps; }
-
-__device__ __forceinline__ void barrier_lds() {
-  // LDS-only barrier: outstanding global loads (the prefetched weights) stay in flight.
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-// Activation preload: the x (and RMSNorm weight) values a wave quantizes -- one float4 per lane
-// per 256-element block, blocks b = wave, wave + NW, ... -- are loaded BEFORE the weight
-// prefetch is issued: vmcnt retires loads in issue order, so the prologue must not wait
-// behind the weights.
-template <int MAXB>
-struct XPre {
-  float4 x[MAXB];
-  float4 w[MAXB];
-};
-
-template <int MAXB>
-__device__ __forceinline__ void preload_x(const GemvArgs& A, XPre<MAXB>& p) {
-  // unconditional loads (indices clamped, a dummy source when there is no norm) so that the
-  // waitcnt pass can count exactly how many later loads may stay in flight
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int nb = A.K / 256;
-  const float4* xs = (const float4*)A.x;
-  const float4* ws = (const float4*)(A.prologue == PRO_RMSNORM ? A.norm_w : A.x);
-#pragma unroll
-  for (int i = 0; i < MAXB; i++) {
-    int b = wid + i * NW;
-    if (b >= nb) b = nb - 1;
-    p.x[i] = xs[b * 64 + lane];
-    p.w[i] = ws[b * 64 + lane];
-  }
-}
-
-// 1/m of rms_norm (candle_nn::ops::rms_norm: m = sqrt(sum(x^2)/dim + eps)).  Every workgroup
-// reduces the whole vector itself from the preloaded registers (each element is owned by
-// exactly one lane of the workgroup).
-template <int MAXB>
-__device__ float rms_denominator(const GemvArgs& A, const XPre<MAXB>& p, float* red) {
-  const int tid = threadIdx.x, wid = tid >> 6;
-  const int nb = A.K / 256;
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < MAXB; i++) {
-    if (wid + i * NW < nb) {
-      const float4 v = p.x[i];
-      ss = fmaf(v.x, v.x, ss);
-      ss = fmaf(v.y, v.y, ss);
-      ss = fmaf(v.z, v.z, ss);
-      ss = fmaf(v.w, v.w, ss);
-    }
-  }
-  ss = wave_sum(ss);
-  if ((tid & 63) == 0) red[wid] = ss;
-  barrier_lds();
-  float t = 0.f;
-#pragma unroll
-  for (int i = 0; i < NW; i++) t += red[i];
-  return sqrtf(t / (float)A.K + eps_of(A));
-}
-
-// Q8_K quantization of one 256-block per wave iteration (BlockQ8K::from_float).
-template <int MAXB>
-__device__ void prologue_q8k(const GemvArgs& A, const XPre<MAXB>& p, const Lds& L) {
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int nb = A.K / QK_K;
-  float m = 1.f;
-  const bool norm = A.prologue == PRO_RMSNORM;
-  if (norm) m = rms_denominator<MAXB>(A, p, L.red);
-#pragma unroll
-  for (int i = 0; i < MAXB; i++) {
-    const int b = wid + i * NW;
-    if (b >= nb) break;
-    float4 v = p.x[i];
-    if (norm) {
-      const float4 w = p.w[i];
-      v.x = v.x / m * w.x;
-      v.y = v.y / m * w.y;
-      v.z = v.z / m * w.z;
-      v.w = v.w / m * w.w;
-    }
-    // the signed value of largest |x|, first occurrence winning ties
-    float amax = fabsf(v.x), mx = v.x;
-    int idx = lane * 4;
-    if (fabsf(v.y) > amax) { amax = fabsf(v.y); mx = v.y; idx = lane * 4 + 1; }
-    if (fabsf(v.z) > amax) { amax = fabsf(v.z); mx = v.z; idx = lane * 4 + 2; }
-    if (fabsf(v.w) > amax) { amax = fabsf(v.w); mx = v.w; idx = lane * 4 + 3; }
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const float oa = __shfl_xor(amax, o, WAVE);
-      const float om = __shfl_xor(mx, o, WAVE);
-      const int oi = __shfl_xor(idx, o, WAVE);
-      if (oa > amax || (oa == amax && oi < idx)) { amax = oa; mx = om; idx = oi; }
-    }
-    int packed = 0, qsum = 0;
-    float d = 0.f;
-    if (amax != 0.f) {
-      const float iscale = -128.f / mx;
-      const float e[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        float r = roundf(iscale * e[j]);
-        r = fminf(r, 127.f);
-        r = fmaxf(r, -128.f);
-        const int q = (int)r;
-        qsum += q;
-        packed |= (q & 0xff) << (8 * j);
-      }
-      d = 1.f / iscale;
-    }
-    L.q32[b * 64 + lane] = packed;
-    qsum += __shfl_xor(qsum, 1, WAVE);
-    qsum += __shfl_xor(qsum, 2, WAVE);
-    if ((lane & 3) == 0) L.s16[b * 16 + (lane >> 2)] = qsum;
-    if (lane == 0) L.d[b] = d;
-  }
-}
-
-// Q8_0 activation quantization (BlockQ8_0::from_float): 8 lanes per 32-block.
-template <int MAXB>
-__device__ void prologue_q80(const GemvArgs& A, const XPre<MAXB>& p, const Lds& L) {
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int nb = A.K / 256;
-  float m = 1.f;
-  const bool norm = A.prologue == PRO_RMSNORM;
-  if (norm) m = rms_denominator<MAXB>(A, p, L.red);
-#pragma unroll
-  for (int i = 0; i < MAXB; i++) {
-    const int c = wid + i * NW;
-    if (c >= nb) break;
-    float4 v = p.x[i];
-    if (norm) {
-      const float4 w = p.w[i];
-      v.x = v.x / m * w.x;
-      v.y = v.y / m * w.y;
-      v.z = v.z / m * w.z;
-      v.w = v.w / m * w.w;
-    }
-    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-#pragma unroll
-    for (int o = 1; o < 8; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, WAVE));
-    const float d = amax / 127.f;
-    const float id = d != 0.f ? 1.f / d : 0.f;
-    const float e[4] = {v.x, v.y, v.z, v.w};
-    int packed = 0;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      float r = roundf(e[j] * id);
-      r = fminf(fmaxf(r, -128.f), 127.f);
-      packed |= ((int)r & 0xff) << (8 * j);
-    }
-    L.q32[c * 64 + lane] = packed;
-    if ((lane & 7) == 0) L.d[c * 8 + (lane >> 3)] = h2f(f2h(d));  // stored as f16
-  }
-}
-
-template <int WT>
-__device__ __forceinline__ void load_act(const Lds& L, int g, Act& a) {
-  if constexpr (WT == TPT_TYPE_Q4_K) {
-#pragma unroll
-    for (int i = 0; i < 16; i++) a.q[i] = L.q32[16 * g + i];
-    a.d0 = L.d[g >> 2];
-    a.s[0] = L.s16[4 * g] + L.s16[4 * g + 1];
-    a.s[1] = L.s16[4 * g + 2] + L.s16[4 * g + 3];
-  } else if constexpr (WT == TPT_TYPE_Q6_K) {
-    const int b = g >> 2, p = (g >> 1) & 1, h = g & 1;
-#pragma unroll
-    for (int quad = 0; quad < 4; quad++) {
-      const int e0 = 256 * b + 128 * p + 32 * quad + 16 * h;
-#pragma unroll
-      for (int i = 0; i < 4; i++) a.q[4 * quad + i] = L.q32[e0 / 4 + i];
-      a.s[quad] = L.s16[e0 / 16];
-    }
-    a.d0 = L.d[b];
-  } else {
-#pragma unroll
-    for (int i = 0; i < 16; i++) a.q[i] = L.q32[16 * g + i];
-    a.d0 = L.d[2 * g];
-    a.d1 = L.d[2 * g + 1];
-  }
-}
-
 // ----------------------------------------------------------------- the kernel
-template <int LPR, int GPL, int NMAT>
-struct Shape {
-  static constexpr int RPW = WAVE / LPR;  // rows per wave pass (one per lane slot)
-  static constexpr int RB = GPL >= 3 ? 1 : (GPL == 2 || NMAT == 2) ? 2 : 4;  // passes/chunk
-  static constexpr int MAXB = (LPR * GPL / 4 + NW - 1) / NW;  // 256-blocks per wave (prologue)
+// Launch geometry shared by host and device.
+struct Geo {
+  int rows_per_wg;  // contiguous rows per workgroup (whole row groups, even)
+  int P;            // passes per row
 };
 
-template <int WT, int LPR, int GPL, int NMAT>
-__global__ void __launch_bounds__(NT) gemv_q8_kernel(const GemvArgs A) {
-  using S = Shape<LPR, GPL, NMAT>;
-  constexpr int RPW = S::RPW, RB = S::RB, MAXB = S::MAXB;
+// WT weight type; BPP super-blocks per row per pass (16, or fewer for short rows, then
+// RPP = 16/BPP rows share a pass); RB row slots per step; NMAT matrices (2: gate|up);
+// KS-way split of the passes across waves; D steps in flight per wave.
+template <int WT, int BPP, int RB, int NMAT, int KS, int D>
+__global__ void __launch_bounds__(NT, 2) gemv_q8_kernel(const GemvArgs A, const Geo geo) {
+  constexpr int RPP = 16 / BPP;   // rows per pass
+  constexpr int LPR = 4 * BPP;    // lanes per row
+  constexpr int RG = RB * RPP;    // rows per row group
+  constexpr int WR = NW / KS;     // waves per k-split
   extern __shared__ __align__(16) char smem[];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int slot = lane / LPR, lr = lane % LPR;
-  const int K = A.K, N = A.N, G = K / 64;
-  const Lds L = lds_layout(smem, K, WT == TPT_TYPE_Q8_0);
+  const int K = A.K, N = A.N;
+  const bool q80 = WT == TPT_TYPE_Q8_0;
+  const int nb = K / QK_K;  // super-blocks (256 weights) per row
+  const Lds L = lds_layout(smem, K, q80);
+  const int RPW = geo.rows_per_wg;
+  const int r0 = blockIdx.x * RPW;
+  const int rp = lane / LPR, sb = (lane / 4) % BPP, q = lane & 3;
 
-  // contiguous chunk range of this wave; a chunk = RB*RPW consecutive rows
-  const long units = (N + RPW - 1) / RPW;
-  const long chunks = (units + RB - 1) / RB;
-  const long W = (long)gridDim.x * NW, gw = (long)blockIdx.x * NW + wid;
-  const long c_begin = gw * chunks / W, c_end = (gw + 1) * chunks / W;
+  // this wave's row groups and passes
+  const int ngrp = RPW / RG;
+  const int wr = wid / KS, ks = wid % KS;
+  const int g0 = wr * ngrp / WR, g1 = (wr + 1) * ngrp / WR;
+  const int pa = ks * geo.P / KS, pb = (ks + 1) * geo.P / KS;
+  const int PP = pb - pa;
+  const int S = (g1 - g0) * PP;
 
-  // 1. activation values this wave quantizes (issued first: see preload_x)
-  XPre<MAXB> xp;
-  preload_x<MAXB>(A, xp);
-  int pos = 0;
-  if (A.epilogue == EPI_ROPE_QKV) pos = A.state ? A.state->pos : A.pos_host;
+  // 1. activation values (issued first: see preload_x)
+  XPre xp;
+  preload_x(A, xp);
 
-  // 2. weight prefetch of the first chunk
-  Raw<WT> raw[RB][GPL][NMAT];
-  auto issue = [&](long c) {
+  // 2. the first D steps' weight loads, then the prologue under their latency.  Steps live in
+  //    a ring of D register slots; slot d holds steps d, d + D, d + 2D, ...
+  Raw<WT> ring[D][RB][NMAT];
+  auto group_of = [&](int p, bool* valid) {  // this lane's weight group in pass p
+    const int blk = p * BPP + sb;
+    *valid = blk < nb;
+    return 4 * (blk < nb ? blk : nb - 1) + q;
+  };
+  auto issue = [&](Raw<WT> (&buf)[RB][NMAT], int s) {
+    if (s >= S) s = S > 0 ? S - 1 : 0;  // past the end: re-read the last step (cache hits)
+    const int pp = PP > 0 ? PP : 1;
+    const int grp = g0 + s / pp, p = pa + s % pp;
+    bool v;
+    const int g = group_of(p, &v);
 #pragma unroll
-    for (int r = 0; r < RB; r++) {
-      long row = (c * RB + r) * RPW + slot;
-      if (row >= N) row = N - 1;  // clamp: loads stay in bounds, result discarded
+    for (int j = 0; j < RB; j++) {
+      int row = r0 + (grp * RB + j) * RPP + rp;
+      if (row >= N) row = N - 1;
 #pragma unroll
-      for (int j = 0; j < GPL; j++) {
-        int g = lr + j * LPR;
-        if (g >= G) g = G - 1;
-#pragma unroll
-        for (int m = 0; m < NMAT; m++) {
-          const uint8_t* base = (m == 0 ? A.w0 : A.w1) + (size_t)row * A.row_stride;
-          load_raw<WT>(base, g, raw[r][j][m]);
-        }
-      }
+      for (int m = 0; m < NMAT; m++)
+        load_raw<WT>((m == 0 ? A.w0 : A.w1) + (size_t)row * A.row_stride, g, buf[j][m]);
     }
   };
-  issue(c_begin < c_end ? c_begin : (chunks > 0 ? chunks - 1 : 0));  // unconditional (see preload_x)
-
-  // 3. activation quantization into LDS (runs under the prefetch's latency)
-  if constexpr (WT == TPT_TYPE_Q8_0) prologue_q80<MAXB>(A, xp, L);
-  else prologue_q8k<MAXB>(A, xp, L);
+#pragma unroll
+  for (int d = 0; d < D; d++) issue(ring[d], d);
+  if constexpr (WT == TPT_TYPE_Q8_0) prologue_q80(A, xp, L);
+  else prologue_q8k(A, xp, L);
   barrier_lds();
 
-  Act act[GPL];
+  float acc[RB][NMAT];
 #pragma unroll
-  for (int j = 0; j < GPL; j++) {
-    const int g = lr + j * LPR;
-    load_act<WT>(L, g < G ? g : G - 1, act[j]);
-  }
+  for (int j = 0; j < RB; j++)
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) acc[j][m] = 0.f;
 
-  unsigned long long best = 0;
-  for (long c = c_begin; c < c_end; c++) {
-    // epilogue inputs of this chunk, loaded before the next chunk's weights are issued
-    // (unconditionally, from a dummy address when unused)
-    float ein0[RB], ein1[RB];
+  auto compute = [&](const Raw<WT> (&buf)[RB][NMAT], int s) {
+    const int grp = g0 + s / PP, p = pa + s % PP;
+    bool v;
+    const int g = group_of(p, &v);
+    Act act;
+    load_act<WT>(L, g, act);
 #pragma unroll
-    for (int r = 0; r < RB; r++) {
-      long row = (c * RB + r) * RPW + slot;
-      if (row >= N) row = N - 1;
-      const float* p0 = A.x;
-      const float* p1 = A.x;
-      if (A.epilogue == EPI_RESID) {
-        p0 = A.resid + row;
-      } else if (A.epilogue == EPI_ROPE_QKV) {
-        const int lrow = A.row0 + (int)row;
-        const int rr = lrow < A.qd ? lrow : lrow - A.qd;
-        const size_t ti = (size_t)pos * (A.hd / 2) + ((rr % A.hd) >> 1);
-        p0 = A.rope_cos + ti;
-        p1 = A.rope_sin + ti;
-      }
-      ein0[r] = *p0;
-      ein1[r] = *p1;
-    }
-
-    float acc[RB][NMAT];
-#pragma unroll
-    for (int r = 0; r < RB; r++)
+    for (int j = 0; j < RB; j++)
 #pragma unroll
       for (int m = 0; m < NMAT; m++) {
-        float s = 0.f;
-#pragma unroll
-        for (int j = 0; j < GPL; j++) {
-          const int g = lr + j * LPR;
-          const float v = dot_group(raw[r][j][m], act[j], g);
-          if ((j + 1) * LPR <= G || g < G) s += v;
-        }
-        acc[r][m] = group_sum<LPR>(s);
+        const float t = dot_group(buf[j][m], act, g);
+        acc[j][m] += v ? t : 0.f;
       }
-    issue(c + 1 < c_end ? c + 1 : c);  // next rows' loads overlap this chunk's epilogue
-
+    if (p == pb - 1) {  // row group done: row totals to LDS
 #pragma unroll
-    for (int r = 0; r < RB; r++) {
-      const long row = (c * RB + r) * RPW + slot;
-      const bool valid = row < N && lr == 0;
-      switch (A.epilogue) {
-        case EPI_STORE:
-          if (valid) A.y[row] = acc[r][0];
-          break;
-        case EPI_RESID:
-          if (valid) A.y[row] = acc[r][0] + ein0[r];
-          break;
-        case EPI_SWIGLU:
-          if (valid) {
-            const float g = acc[r][0];
-            A.y[row] = g / (1.f + expf(-g)) * acc[r][NMAT - 1];
-          }
-          break;
-        case EPI_ARGMAX:
-          if (valid) {
-            if (A.y) A.y[row] = acc[r][0];
-            const unsigned long long key =
-                ((unsigned long long)order_key(acc[r][0]) << 32) | (unsigned long long)row;
-            best = key > best ? key : best;
-          }
-          break;
-        case EPI_ROPE_QKV: {
-          // rows come in (even, odd) pairs: consecutive passes when RPW == 1, adjacent slots
-          // (lanes l and l + LPR) otherwise.
-          float partner;
-          bool first;
-          if constexpr (RPW == 1 && RB == 1) {
-            partner = 0.f;  // unreachable: the host rejects RoPE for this layout
-            first = true;
-          } else if constexpr (RPW == 1) {
-            partner = acc[r ^ 1][0];
-            first = (r & 1) == 0;
-          } else {
-            partner = __shfl_xor(acc[r][0], LPR, WAVE);
-            first = (slot & 1) == 0;
-          }
-          if (valid) {
-            const int lrow = A.row0 + (int)row;
-            const float self = acc[r][0];
-            const float x0 = first ? self : partner, x1 = first ? partner : self;
-            if (lrow < A.qd + A.kd) {
-              const bool isq = lrow < A.qd;
-              const int rr = isq ? lrow : lrow - A.qd;
-              const float cs = ein0[r], sn = ein1[r];
-              // candle rope_i: dst[2i] = x0*cos - x1*sin; dst[2i+1] = x0*sin + x1*cos
-              const float out = first ? (x0 * cs - x1 * sn) : (x0 * sn + x1 * cs);
-              if (isq) {
-                A.y[rr] = out;
-              } else {
-                const size_t ci = ((size_t)(rr / A.hd) * A.max_ctx + pos) * A.hd + rr % A.hd;
-                if (A.kv_type == TPT_TYPE_F32) ((float*)A.kcache)[ci] = out;
-                else ((uint16_t*)A.kcache)[ci] = f2h(out);
-              }
-            } else {
-              const int rr = lrow - A.qd - A.kd;
-              const size_t ci = ((size_t)(rr / A.hd) * A.max_ctx + pos) * A.hd + rr % A.hd;
-              if (A.kv_type == TPT_TYPE_F32) ((float*)A.vcache)[ci] = self;
-              else ((uint16_t*)A.vcache)[ci] = f2h(self);
-            }
-          }
-        } break;
+      for (int j = 0; j < RB; j++)
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) {
+          const float t = lane_group_sum<LPR>(acc[j][m]);
+          if (lane % LPR == 0) L.rows[((size_t)ks * RPW + (grp * RB + j) * RPP + rp) * NMAT + m] = t;
+          acc[j][m] = 0.f;
+        }
+    }
+  };
+
+  if (S > 0) {
+    for (int s = 0; s < S; s += D) {
+#pragma unroll
+      for (int d = 0; d < D; d++) {
+        if (s + d < S) compute(ring[d], s + d);
+        issue(ring[d], s + d + D);  // unconditional: the slot's next step
       }
     }
   }
-  if (A.epilogue == EPI_ARGMAX) {
-    // wave max of the 64-bit keys, one atomic per wave
+  __syncthreads();
+
+  // 3. epilogue over the workgroup's rows
+  const int nrows = min(RPW, N - r0);
+  int pos = 0;
+  if (A.epilogue == EPI_ROPE_QKV) pos = A.state ? A.state->pos : A.pos_host;
+  auto row_val = [&](int i, int m) {
+    float t = 0.f;
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const unsigned long long ob = __shfl_xor(best, o, WAVE);
-      best = ob > best ? ob : best;
-    }
-    if (lane == 0 && best) {
-      unsigned long long* slot_p = A.amax + (A.state ? A.state->parity : 0);
-      atomicMax(slot_p, best);
-    }
+    for (int k = 0; k < KS; k++) t += L.rows[((size_t)k * RPW + i) * NMAT + m];
+    return t;
+  };
+  switch (A.epilogue) {
+    case EPI_STORE:
+      for (int i = tid; i < nrows; i += NT) A.y[r0 + i] = row_val(i, 0);
+      break;
+    case EPI_RESID:
+      for (int i = tid; i < nrows; i += NT) A.y[r0 + i] = row_val(i, 0) + A.resid[r0 + i];
+      break;
+    case EPI_SWIGLU:
+      for (int i = tid; i < nrows; i += NT) {
+        const float g = row_val(i, 0);
+        A.y[r0 + i] = g / (1.f + expf(-g)) * row_val(i, NMAT - 1);
+      }
+      break;
+    case EPI_ARGMAX: {
+      unsigned long long best = 0;
+      for (int i = tid; i < nrows; i += NT) {
+        const float v = row_val(i, 0);
+        if (A.y) A.y[r0 + i] = v;
+        const unsigned long long key =
+            ((unsigned long long)order_key(v) << 32) | (unsigned long long)(r0 + i);
+        best = key > best ? key : best;
+      }
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const unsigned long long ob = __shfl_xor(best, o, WAVE);
+        best = ob > best ? ob : best;
+      }
+      // one atomic per workgroup: the waves' maxima meet in LDS (the row buffer is free now)
+      unsigned long long* wbest = (unsigned long long*)L.q32;
+      __syncthreads();
+      if (lane == 0) wbest[wid] = best;
+      __syncthreads();
+      if (tid == 0) {
+        unsigned long long b = 0;
+#pragma unroll
+        for (int w = 0; w < NW; w++) b = wbest[w] > b ? wbest[w] : b;
+        if (b) atomicMax(A.amax + (A.state ? A.state->parity : 0), b);
+      }
+    } break;
+    case EPI_ROPE_QKV:
+      // rows come in (even, odd) pairs; r0 and nrows are even
+      for (int i = 2 * tid; i < nrows; i += 2 * NT) {
+        const float x0 = row_val(i, 0), x1 = row_val(i + 1, 0);
+        const int lrow = A.row0 + r0 + i;
+        if (lrow < A.qd + A.kd) {
+          const bool isq = lrow < A.qd;
+          const int rr = isq ? lrow : lrow - A.qd;
+          const size_t ti = (size_t)pos * (A.hd / 2) + ((rr % A.hd) >> 1);
+          const float cs = A.rope_cos[ti], sn = A.rope_sin[ti];
+          // candle rope_i: dst[2i] = x0*cos - x1*sin; dst[2i+1] = x0*sin + x1*cos
+          const float o0 = x0 * cs - x1 * sn, o1 = x0 * sn + x1 * cs;
+          if (isq) {
+            A.y[rr] = o0;
+            A.y[rr + 1] = o1;
+          } else {
+            const size_t ci = ((size_t)(rr / A.hd) * A.max_ctx + pos) * A.hd + rr % A.hd;
+            if (A.kv_type == TPT_TYPE_F32) {
+              ((float*)A.kcache)[ci] = o0;
+              ((float*)A.kcache)[ci + 1] = o1;
+            } else {
+              ((uint16_t*)A.kcache)[ci] = f2h(o0);
+              ((uint16_t*)A.kcache)[ci + 1] = f2h(o1);
+            }
+          }
+        } else {
+          const int rr = lrow - A.qd - A.kd;
+          const size_t ci = ((size_t)(rr / A.hd) * A.max_ctx + pos) * A.hd + rr % A.hd;
+          if (A.kv_type == TPT_TYPE_F32) {
+            ((float*)A.vcache)[ci] = x0;
+            ((float*)A.vcache)[ci + 1] = x1;
+          } else {
+            ((uint16_t*)A.vcache)[ci] = f2h(x0);
+            ((uint16_t*)A.vcache)[ci + 1] = f2h(x1);
+          }
+        }
+      }
+      break;
   }
 }
 
@@ -549,6 +573,7 @@ __global__ void __launch_bounds__(NT) gemv_q8_kernel(const GemvArgs A) {
 // y[r] = sum_k dequant(W)[r,k] * x[k] (dequantized exactly like the oracle, fp32 FMA).  One
 // wave per row, x read through the vector cache.  Not on the parity path (candle quantizes
 // activations); kept for the fp32-activation GEMV report.
+// (The group layout and loads are the ones the Q8 kernel uses.)
 template <int WT>
 __device__ __forceinline__ void dequant64(const uint8_t* row, int g, float* y);
 
@@ -653,50 +678,54 @@ __global__ void __launch_bounds__(256) gemv_f32_kernel(const uint8_t* __restrict
   if (lane == 0) y[row] = acc;
 }
 
-template <int WT, int LPR, int GPL, int NMAT>
-int launch_one(const tpt_ctx* ctx, const GemvArgs& a, hipStream_t s) {
-  const bool q80 = WT == TPT_TYPE_Q8_0;
-  const size_t lds = (size_t)a.K + 4 * (q80 ? a.K / QK8_0 : a.K / QK_K) + 4 * (a.K / 16) + 4 * NW;
-  constexpr int RPW = Shape<LPR, GPL, NMAT>::RPW, RB = Shape<LPR, GPL, NMAT>::RB;
-  const long chunks = ((a.N + RPW - 1) / RPW + RB - 1) / RB;
-  long grid = (chunks + NW - 1) / NW;
-  const long cap = ctx && ctx->n_cu > 0 ? ctx->n_cu : 256;
-  if (grid > cap) grid = cap;
-  if (grid < 1) grid = 1;
-  hipLaunchKernelGGL((gemv_q8_kernel<WT, LPR, GPL, NMAT>), dim3((unsigned)grid), dim3(NT), lds, s, a);
+// ----------------------------------------------------------------- launch
+template <int WT, int BPP, int RB, int NMAT, int KS, int D>
+int launch_cfg(const tpt_ctx* ctx, const GemvArgs& a, int wg_per_cu, hipStream_t s) {
+  Geo geo;
+  const int nb = a.K / QK_K;
+  geo.P = (nb + BPP - 1) / BPP;
+  if (KS > geo.P) return fail(TPT_ERR_INVALID, "gemv: K split larger than the passes per row");
+  const int ncu = ctx && ctx->n_cu > 0 ? ctx->n_cu : 256;
+  const int cap = ncu * (wg_per_cu > 0 ? wg_per_cu : 1);
+  const int rg = RB * (16 / BPP);
+  const int unit = rg >= 2 ? rg : 2;  // whole row groups, even row ranges (RoPE pairs)
+  int rpw = (a.N + cap - 1) / cap;
+  rpw = (rpw + unit - 1) / unit * unit;
+  geo.rows_per_wg = rpw;
+  const int grid = (a.N + rpw - 1) / rpw;
+  const size_t lds = lds_act_bytes(a.K, WT == TPT_TYPE_Q8_0) + 4 * (size_t)KS * rpw * NMAT;
+  if (lds > 65536) return fail(TPT_ERR_UNSUPPORTED, "gemv: too many rows per workgroup for LDS");
+  hipLaunchKernelGGL((gemv_q8_kernel<WT, BPP, RB, NMAT, KS, D>), dim3((unsigned)grid), dim3(NT), lds, s, a, geo);
   TPT_HIP(hipGetLastError());
   return TPT_OK;
 }
 
+// Launch shape by matrix shape: BPP from the row length (short rows share a pass), RB rows per
+// step, D steps in flight per wave, one workgroup per CU.
+template <int WT, int NMAT, int RB, int D>
+int by_bpp(const tpt_ctx* ctx, const GemvArgs& a, hipStream_t s) {
+  const int nb = a.K / QK_K;
+  if (nb >= 16) return launch_cfg<WT, 16, RB, NMAT, 1, D>(ctx, a, 1, s);
+  if (nb >= 8) return launch_cfg<WT, 8, RB, NMAT, 1, D>(ctx, a, 1, s);
+  if (nb >= 4) return launch_cfg<WT, 4, RB, NMAT, 1, D>(ctx, a, 1, s);
+  if (nb >= 2) return launch_cfg<WT, 2, RB, NMAT, 1, D>(ctx, a, 1, s);
+  return launch_cfg<WT, 1, RB, NMAT, 1, D>(ctx, a, 1, s);
+}
+
 template <int WT, int NMAT>
-int dispatch_layout(const tpt_ctx* ctx, const GemvArgs& a, hipStream_t s) {
-  const int G = a.K / 64;
-  if (G >= 64) {
-    const int gpl = (G + 63) / 64;
-    switch (gpl) {
-      case 1: return launch_one<WT, 64, 1, NMAT>(ctx, a, s);
-      case 2: return launch_one<WT, 64, 2, NMAT>(ctx, a, s);
-      case 3:
-      case 4:
-        if constexpr (NMAT == 1) {
-          if (a.epilogue == EPI_ROPE_QKV) return fail(TPT_ERR_UNSUPPORTED, "gemv: RoPE epilogue needs K <= 8192");
-          return gpl == 3 ? launch_one<WT, 64, 3, 1>(ctx, a, s) : launch_one<WT, 64, 4, 1>(ctx, a, s);
-        }
-        return fail(TPT_ERR_UNSUPPORTED, "gemv: two-matrix epilogue needs K <= 8192");
-      default: return fail(TPT_ERR_UNSUPPORTED, "gemv: K > 16384 not supported");
-    }
+int dispatch_shape(const tpt_ctx* ctx, const GemvArgs& a, hipStream_t s) {
+  if constexpr (NMAT == 2) return by_bpp<WT, 2, 1, 2>(ctx, a, s);
+  else {
+    if (a.K > 8192) return by_bpp<WT, 1, 2, 2>(ctx, a, s);  // long rows: two rows per step
+    return by_bpp<WT, 1, 1, 2>(ctx, a, s);
   }
-  if (G >= 32) return G == 32 ? launch_one<WT, 32, 1, NMAT>(ctx, a, s) : launch_one<WT, 32, 2, NMAT>(ctx, a, s);
-  if (G >= 16) return G == 16 ? launch_one<WT, 16, 1, NMAT>(ctx, a, s) : launch_one<WT, 16, 2, NMAT>(ctx, a, s);
-  if (G >= 8) return G == 8 ? launch_one<WT, 8, 1, NMAT>(ctx, a, s) : launch_one<WT, 8, 2, NMAT>(ctx, a, s);
-  if (G >= 4) return G == 4 ? launch_one<WT, 4, 1, NMAT>(ctx, a, s) : launch_one<WT, 4, 2, NMAT>(ctx, a, s);
-  return fail(TPT_ERR_UNSUPPORTED, "gemv: K must be a multiple of 256 (>= 256)");
 }
 
 }  // namespace
 
 int launch_gemv_q8(const tpt_ctx* ctx, int wtype, const GemvArgs& a, hipStream_t s) {
   if (a.K <= 0 || a.N <= 0 || a.K % 256) return fail(TPT_ERR_INVALID, "gemv: K must be a positive multiple of 256, N > 0");
+  if (a.K > 64 * 256) return fail(TPT_ERR_UNSUPPORTED, "gemv: K > 16384 not supported");
   if (!a.w0 || !a.x) return fail(TPT_ERR_INVALID, "gemv: null weight/activation pointer");
   if (a.prologue == PRO_RMSNORM && !a.norm_w) return fail(TPT_ERR_INVALID, "gemv: rmsnorm prologue needs norm weights");
   if (a.epilogue == EPI_SWIGLU && !a.w1) return fail(TPT_ERR_INVALID, "gemv: swiglu needs two matrices");
@@ -704,9 +733,9 @@ int launch_gemv_q8(const tpt_ctx* ctx, int wtype, const GemvArgs& a, hipStream_t
     return fail(TPT_ERR_INVALID, "gemv: rope epilogue needs even row counts");
   const bool two = a.epilogue == EPI_SWIGLU;
   switch (wtype) {
-    case TPT_TYPE_Q4_K: return two ? dispatch_layout<TPT_TYPE_Q4_K, 2>(ctx, a, s) : dispatch_layout<TPT_TYPE_Q4_K, 1>(ctx, a, s);
-    case TPT_TYPE_Q6_K: return two ? dispatch_layout<TPT_TYPE_Q6_K, 2>(ctx, a, s) : dispatch_layout<TPT_TYPE_Q6_K, 1>(ctx, a, s);
-    case TPT_TYPE_Q8_0: return two ? dispatch_layout<TPT_TYPE_Q8_0, 2>(ctx, a, s) : dispatch_layout<TPT_TYPE_Q8_0, 1>(ctx, a, s);
+    case TPT_TYPE_Q4_K: return two ? dispatch_shape<TPT_TYPE_Q4_K, 2>(ctx, a, s) : dispatch_shape<TPT_TYPE_Q4_K, 1>(ctx, a, s);
+    case TPT_TYPE_Q6_K: return two ? dispatch_shape<TPT_TYPE_Q6_K, 2>(ctx, a, s) : dispatch_shape<TPT_TYPE_Q6_K, 1>(ctx, a, s);
+    case TPT_TYPE_Q8_0: return two ? dispatch_shape<TPT_TYPE_Q8_0, 2>(ctx, a, s) : dispatch_shape<TPT_TYPE_Q8_0, 1>(ctx, a, s);
   }
   return fail(TPT_ERR_UNSUPPORTED, "gemv: weight type must be Q4_K, Q6_K or Q8_0");
 }

@@ -55,10 +55,14 @@ __global__ void dequant_kernel(int type, const uint8_t* __restrict__ w, float* _
     y[i] = dequant_elem(type, w, i);
 }
 
+// Decode-step prologue (one workgroup): the token of this position (prompt, host override or
+// the previous step's argmax), then its embedding row: the row's bytes are staged in LDS with
+// independent 2-byte loads (every GGUF row length here is even) and dequantized from there.
 __global__ void __launch_bounds__(256) step_begin_kernel(StepState* st, const uint32_t* prompt,
                                                          int embd_type, const uint8_t* embd,
                                                          size_t embd_row_bytes, int H, int vocab,
                                                          float* x, uint32_t* tok_log) {
+  extern __shared__ __align__(16) uint16_t s_row[];
   __shared__ uint32_t s_tok;
   __shared__ int s_pos;
   if (threadIdx.x == 0) {
@@ -72,8 +76,11 @@ __global__ void __launch_bounds__(256) step_begin_kernel(StepState* st, const ui
     s_pos = pos;
   }
   __syncthreads();
-  const uint8_t* row = embd + (size_t)s_tok * embd_row_bytes;
-  for (int i = threadIdx.x; i < H; i += blockDim.x) x[i] = dequant_elem(embd_type, row, i);
+  const uint16_t* row = (const uint16_t*)(embd + (size_t)s_tok * embd_row_bytes);
+  const int nh = (int)(embd_row_bytes / 2);
+  for (int i = threadIdx.x; i < nh; i += blockDim.x) s_row[i] = row[i];
+  __syncthreads();
+  for (int i = threadIdx.x; i < H; i += blockDim.x) x[i] = dequant_elem(embd_type, (const uint8_t*)s_row, i);
   if (threadIdx.x == 0) {
     const int np = st->parity ^ 1;
     st->pos = s_pos;
@@ -166,8 +173,10 @@ int launch_dequant(int type, const void* w, float* y, int64_t n, hipStream_t s) 
 int launch_step_begin(StepState* st, const uint32_t* prompt, int embd_type, const uint8_t* embd,
                       size_t embd_row_bytes, int H, int vocab, float* x, uint32_t* tok_log,
                       hipStream_t s) {
-  hipLaunchKernelGGL(step_begin_kernel, dim3(1), dim3(256), 0, s, st, prompt, embd_type, embd,
-                     embd_row_bytes, H, vocab, x, tok_log);
+  if (embd_row_bytes % 2 || embd_row_bytes > 65536)
+    return fail(TPT_ERR_UNSUPPORTED, "embedding rows must be of even length and at most 64 KB");
+  hipLaunchKernelGGL(step_begin_kernel, dim3(1), dim3(256), embd_row_bytes, s, st, prompt,
+                     embd_type, embd, embd_row_bytes, H, vocab, x, tok_log);
   TPT_HIP(hipGetLastError());
   return TPT_OK;
 }

@@ -72,10 +72,13 @@ struct AttnArgs {
   int L_host = 0;                    // used when state == nullptr
   const StepState* state = nullptr;  // L = state->pos + 1
   int n_chunks = 0;
+  int chunk_len = 0;                 // positions per chunk (multiple of 16, <= 1024); chunk c
+                                     // covers [c*chunk_len, (c+1)*chunk_len) clipped to L
   float* part = nullptr;             // [nkv][n_chunks][G][hd + 2] chunk records
 };
 int attn_part_floats(int nq, int nkv, int hd, int n_chunks);
 int attn_default_chunks(int L, int nkv);
+int attn_chunk_len(int L, int n_chunks);  // smallest multiple of 16 covering L in n_chunks
 int attn_max_len();  // longest cache the split-K partition supports
 int launch_attn_decode(const AttnArgs& a, hipStream_t s);
 

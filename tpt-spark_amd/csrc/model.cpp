@@ -294,13 +294,17 @@ int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_t
   return TPT_OK;
 }
 
-int tpt_model::chunks_for(int L) const {
+// Attention partition of the length bucket holding L (powers of two from 64): the chunk count
+// and chunk length are fixed per bucket, so one captured graph serves every length in it.
+int tpt_model::bucket_of(int L) const {
   int b = 64;
   while (b < L) b *= 2;
-  return std::min(attn_default_chunks(b, desc.n_kv_heads), attn_max_chunks);
+  return b;
 }
 
-int tpt_model::enqueue_step(int n_chunks, bool lm_head) {
+int tpt_model::enqueue_step(int bucket, bool lm_head) {
+  const int n_chunks = std::min(attn_default_chunks(bucket, desc.n_kv_heads), attn_max_chunks);
+  const int chunk_len = attn_chunk_len(bucket, n_chunks);
   const int H = desc.embed, hd = desc.head_dim, nq = desc.n_heads, nkv = desc.n_kv_heads;
   const int qd = nq * hd, kd = nkv * hd, F = desc.ffn, mc = desc.max_ctx;
   int rc = launch_step_begin(st, prompt_dev, embd_type, embd, embd_row, H, desc.vocab, x, tok_log, stream);
@@ -358,6 +362,7 @@ int tpt_model::enqueue_step(int n_chunks, bool lm_head) {
     at.L_stride = mc;
     at.state = st;
     at.n_chunks = n_chunks;
+    at.chunk_len = chunk_len;
     at.part = attn_part;
     if ((rc = launch_attn_decode(at, stream))) return rc;
     // x += Wo . attn
@@ -418,7 +423,7 @@ int tpt_model::enqueue_step(int n_chunks, bool lm_head) {
 
 int tpt_model::launch_step(int L, bool lm_head) {
   if (L > desc.max_ctx) return fail(TPT_ERR_STATE, "context length exhausted");
-  const int nch = chunks_for(L);
+  const int nch = bucket_of(L);
   if (!use_graphs || !lm_head) return enqueue_step(nch, lm_head);
   auto it = graphs.find(nch);
   if (it == graphs.end()) {

@@ -47,14 +47,14 @@ struct tpt_model {
   tpt::StepState* st_host = nullptr;  // pinned
   uint32_t* ids_host = nullptr;       // pinned staging for prompt ids [max_ctx]
   bool use_graphs = true;
-  std::map<int, hipGraphExec_t> graphs;  // by attention chunk count
+  std::map<int, hipGraphExec_t> graphs;  // by length bucket
 
   ~tpt_model();
   int load(tpt_ctx* c, const char* gguf_path, int max_ctx, int kv_type, tpt_progress_fn progress,
            void* user);
-  int enqueue_step(int n_chunks, bool lm_head);
+  int enqueue_step(int bucket, bool lm_head);
   int launch_step(int L, bool lm_head);  // graph replay (or direct launches)
-  int chunks_for(int L) const;
+  int bucket_of(int L) const;
   int set_state(int next_pos, int prompt_len, int use_override, uint32_t tok);
   int read_state(tpt::StepState* out);
   int prefill(const uint32_t* ids, int n, int pos0, uint32_t* next_out, float* logits_out);

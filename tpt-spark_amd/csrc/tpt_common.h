@@ -83,11 +83,30 @@ __device__ __forceinline__ float sum16(float v) {
 }
 template <int W>
 __device__ __forceinline__ float lane_group_sum(float v) {  // aligned groups of W lanes
-  static_assert(W == 16 || W == 32 || W == 64, "group of 16, 32 or 64 lanes");
-  v = sum16(v);
+  static_assert(W == 4 || W == 8 || W == 16 || W == 32 || W == 64, "group of 4 .. 64 lanes");
+  v += dpp_mov<0xB1>(v);                        // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4E>(v);                        // quad_perm [2,3,0,1]
+  if constexpr (W >= 8) v += dpp_mov<0x141>(v);   // row_half_mirror
+  if constexpr (W >= 16) v += dpp_mov<0x140>(v);  // row_mirror
   if constexpr (W >= 32) v += __shfl_xor(v, 16, WAVE);
   if constexpr (W >= 64) v += __shfl_xor(v, 32, WAVE);
   return v;
+}
+// Wave-wide max / sum without LDS: DPP within each 16-lane row, then the four row values
+// through readlane (the result is identical on every lane).
+__device__ __forceinline__ float readlane_f(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));
+  v = fmaxf(v, dpp_mov<0x4E>(v));
+  v = fmaxf(v, dpp_mov<0x141>(v));
+  v = fmaxf(v, dpp_mov<0x140>(v));
+  return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v = sum16(v);
+  return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
 }
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
