@@ -12,8 +12,9 @@ tokens_per_sec = tokens_generated / decode_s with decode timed from the first to
 the timed region.
 
 roofline: the Q4_K fused dequant-GEMV at 4096 -> 14336 (the gate/up shape), timed with HIP
-events on the context's stream over back-to-back launches that rotate through distinct weight
-copies (> 1 GB, more than the 256 MB Infinity Cache).  Algorithmic bytes per launch =
+start/stop events that each dispatch timestamps itself (hipExtLaunchKernelGGL) on the
+context's stream, over back-to-back launches that rotate through distinct weight copies
+(> 1 GB, more than the 256 MB Infinity Cache).  Algorithmic bytes per launch =
 K*N*144/256 + 4K + 4N.  traffic comes from the committed rocprofv3 PMC summary when present.
 
 cpu_baseline: the CPU oracle's restatement of candle's CPU decode (Q8_K activation quant,
@@ -40,6 +41,22 @@ SEED = 20261201
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+COPY_BYTES = 256 << 20
+
+
+def copy_calibration(ctx, iters=4):
+    """A plain 16-byte vector copy of COPY_BYTES (read) into another buffer (write): the
+    reference kernel whose FETCH_SIZE / WRITE_SIZE counters calibrate the GEMV's."""
+    src, dst = ctx.alloc(COPY_BYTES), ctx.alloc(COPY_BYTES)
+    ctx.bench_copy(dst, src, COPY_BYTES, 1)  # first touch of both buffers
+    ms = ctx.bench_copy(dst, src, COPY_BYTES, iters)
+    src.free()
+    dst.free()
+    gbs = 2 * COPY_BYTES / (ms / iters * 1e-3) / 1e9
+    log(f"copy {COPY_BYTES >> 20} MiB: {ms / iters * 1e3:.1f} us/launch, {gbs:.0f} GB/s read+write")
+    return {"bytes_read": COPY_BYTES, "bytes_written": COPY_BYTES, "us_per_launch": round(ms / iters * 1e3, 2)}
 
 
 def gemv_roofline(tp, ctx, iters=256):
@@ -86,14 +103,22 @@ def cpu_baseline(path, budget_s=20.0):
                       f"({dt:.1f} s) on {threads} host threads"}
 
 
-def traffic_from_profiles(key):
-    p = os.path.join(ROOT, "profiles", "gemv_q4k_traffic.json")
+def traffic_from_profiles(shape):
+    """HBM bytes per launch of the Q4_K GEMV at `shape` ("KxN"): FETCH_SIZE + WRITE_SIZE from
+    the committed rocprofv3 PMC summary, each scaled by the copy-kernel calibration there (a
+    line `hbm_bytes_per_launch KxN: <bytes>`); None when the summary is absent."""
+    p = os.path.join(ROOT, "profiles", "gemv_q4k_pmc_traffic.md")
     if not os.path.exists(p):
         return None
-    try:
-        return json.load(open(p)).get(key, {}).get("hbm_bytes_per_launch")
-    except (OSError, ValueError):
-        return None
+    key = f"hbm_bytes_per_launch {shape}:"
+    for line in open(p):
+        line = line.strip().strip("`")
+        if line.startswith(key):
+            try:
+                return int(line[len(key):].strip())
+            except ValueError:
+                return None
+    return None
 
 
 def main():
@@ -105,7 +130,8 @@ def main():
     ap.add_argument("--model", default="", help="existing GGUF (default: generate the 8B shape)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--leg", choices=["all", "gemv"], default="all",
-                    help="gemv: only the GEMV roofline leg (for PMC profiling)")
+                    help="gemv: only the GEMV roofline leg and the copy calibration (profiling)")
+    ap.add_argument("--gemv-iters", type=int, default=256, help="timed launches per GEMV shape")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -118,9 +144,9 @@ def main():
 
     ctx = tp.Context(0)
     log(f"device: {ctx.name}, {ctx.n_cu} CUs")
-    gemv = gemv_roofline(tp, ctx)
+    gemv = gemv_roofline(tp, ctx, iters=args.gemv_iters)
     if args.leg == "gemv":
-        print(json.dumps({"gemv": gemv}))
+        print(json.dumps({"gemv": gemv, "copy": copy_calibration(ctx)}))
         return
 
     tmpdir = tempfile.mkdtemp(prefix="tpt_bench_", dir=os.environ.get("TPT_BENCH_DIR") or None)

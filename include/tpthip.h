@@ -110,8 +110,9 @@ int tpt_argmax(tpt_ctx* ctx, const float* logits, int64_t n, uint32_t* out_host)
 /* ------------------------------------------------------------------ measurement */
 /* No reference counterpart (the reference publishes no kernel timings): these time kernels
  * with HIP events recorded on the context's own stream. */
-/* iters launches of tpt_gemv, launch i reading weights[i % n_weights] (distinct copies defeat
- * the 256 MB Infinity Cache); *ms_out = total event time of the launches. */
+/* iters (<= 4096) back-to-back launches of tpt_gemv, launch i reading weights[i % n_weights]
+ * (distinct copies defeat the 256 MB Infinity Cache); *ms_out = the sum over launches of the
+ * interval between the start and stop events each dispatch timestamps itself. */
 int tpt_bench_gemv(tpt_ctx* ctx, int type, const void* const* weights, int n_weights,
                    const float* x, float* y, int K, int N, int iters, float* ms_out);
 /* iters launches of tpt_attn_decode over the same cache; *ms_out = total event time */

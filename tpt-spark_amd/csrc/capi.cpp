@@ -3,6 +3,7 @@
 
 #include <cmath>
 #include <string>
+#include <vector>
 
 #include "kernels.h"
 
@@ -267,7 +268,7 @@ int tpt_argmax(tpt_ctx* c, const float* logits, int64_t n, uint32_t* out_host) {
 int tpt_bench_gemv(tpt_ctx* c, int type, const void* const* weights, int n_weights,
                    const float* x, float* y, int K, int N, int iters, float* ms_out) {
   ENTER(c);
-  if (!weights || n_weights <= 0 || iters <= 0 || !x || !y || !ms_out)
+  if (!weights || n_weights <= 0 || iters <= 0 || iters > 4096 || !x || !y || !ms_out)
     return fail(TPT_ERR_INVALID, "bench_gemv: bad arguments");
   GemvArgs a;
   a.row_stride = row_bytes(type, K);
@@ -275,22 +276,30 @@ int tpt_bench_gemv(tpt_ctx* c, int type, const void* const* weights, int n_weigh
   a.N = N;
   a.x = x;
   a.y = y;
-  hipEvent_t e0, e1;
-  TPT_HIP(hipEventCreate(&e0));
-  TPT_HIP(hipEventCreate(&e1));
+  // every launch carries its own start/stop events, timestamped by the dispatch packet itself
+  // (hipExtLaunchKernelGGL), so the launches stay back to back and the sum of the intervals is
+  // the kernels' own time
+  std::vector<hipEvent_t> ev((size_t)2 * iters, nullptr);
+  hipError_t e = hipSuccess;
+  for (auto& v : ev)
+    if (e == hipSuccess) e = hipEventCreate(&v);
   int rc = TPT_OK;
-  hipError_t e = hipEventRecord(e0, c->stream);
   for (int i = 0; i < iters && rc == TPT_OK && e == hipSuccess; i++) {
     a.w0 = (const uint8_t*)weights[i % n_weights];
-    rc = launch_gemv_q8(c, type, a, c->stream);
+    rc = launch_gemv_q8(c, type, a, c->stream, ev[2 * i], ev[2 * i + 1]);
   }
-  if (e == hipSuccess) e = hipEventRecord(e1, c->stream);
-  if (e == hipSuccess) e = hipEventSynchronize(e1);
-  if (e == hipSuccess && rc == TPT_OK) e = hipEventElapsedTime(ms_out, e0, e1);
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
+  if (e == hipSuccess && rc == TPT_OK) e = hipEventSynchronize(ev.back());
+  float total = 0.f;
+  for (int i = 0; i < iters && e == hipSuccess && rc == TPT_OK; i++) {
+    float ms = 0.f;
+    e = hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]);
+    total += ms;
+  }
+  for (auto& v : ev)
+    if (v) (void)hipEventDestroy(v);
   if (rc) return rc;
   if (e != hipSuccess) return hip_fail(e, "bench_gemv", __FILE__, __LINE__);
+  *ms_out = total;
   return TPT_OK;
 }
 

@@ -29,6 +29,8 @@
 //    DPP.  Row results go to LDS, and after a workgroup barrier the epilogue stores them:
 //    plain, + residual, SiLU(gate)*up, interleaved RoPE + KV-cache append, or greedy argmax
 //    (what follows the GEMV in run_forward_pass, wgpu_engine.rs:373-486).
+#include <hip/hip_ext.h>
+
 #include "kernels.h"
 
 namespace tpt {
@@ -680,7 +682,8 @@ __global__ void __launch_bounds__(256) gemv_f32_kernel(const uint8_t* __restrict
 
 // ----------------------------------------------------------------- launch
 template <int WT, int BPP, int RB, int NMAT, int KS, int D>
-int launch_cfg(const tpt_ctx* ctx, const GemvArgs& a, int wg_per_cu, hipStream_t s) {
+int launch_cfg(const tpt_ctx* ctx, const GemvArgs& a, int wg_per_cu, hipStream_t s,
+               hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr) {
   Geo geo;
   const int nb = a.K / QK_K;
   geo.P = (nb + BPP - 1) / BPP;
@@ -695,7 +698,11 @@ int launch_cfg(const tpt_ctx* ctx, const GemvArgs& a, int wg_per_cu, hipStream_t
   const int grid = (a.N + rpw - 1) / rpw;
   const size_t lds = lds_act_bytes(a.K, WT == TPT_TYPE_Q8_0) + 4 * (size_t)KS * rpw * NMAT;
   if (lds > 65536) return fail(TPT_ERR_UNSUPPORTED, "gemv: too many rows per workgroup for LDS");
-  hipLaunchKernelGGL((gemv_q8_kernel<WT, BPP, RB, NMAT, KS, D>), dim3((unsigned)grid), dim3(NT), lds, s, a, geo);
+  if (ev0 || ev1)  // the dispatch itself timestamps the events (no packets between kernels)
+    hipExtLaunchKernelGGL((gemv_q8_kernel<WT, BPP, RB, NMAT, KS, D>), dim3((unsigned)grid), dim3(NT), lds, s,
+                          ev0, ev1, 0, a, geo);
+  else
+    hipLaunchKernelGGL((gemv_q8_kernel<WT, BPP, RB, NMAT, KS, D>), dim3((unsigned)grid), dim3(NT), lds, s, a, geo);
   TPT_HIP(hipGetLastError());
   return TPT_OK;
 }
@@ -703,27 +710,28 @@ int launch_cfg(const tpt_ctx* ctx, const GemvArgs& a, int wg_per_cu, hipStream_t
 // Launch shape by matrix shape: BPP from the row length (short rows share a pass), RB rows per
 // step, D steps in flight per wave, one workgroup per CU.
 template <int WT, int NMAT, int RB, int D>
-int by_bpp(const tpt_ctx* ctx, const GemvArgs& a, hipStream_t s) {
+int by_bpp(const tpt_ctx* ctx, const GemvArgs& a, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
   const int nb = a.K / QK_K;
-  if (nb >= 16) return launch_cfg<WT, 16, RB, NMAT, 1, D>(ctx, a, 1, s);
-  if (nb >= 8) return launch_cfg<WT, 8, RB, NMAT, 1, D>(ctx, a, 1, s);
-  if (nb >= 4) return launch_cfg<WT, 4, RB, NMAT, 1, D>(ctx, a, 1, s);
-  if (nb >= 2) return launch_cfg<WT, 2, RB, NMAT, 1, D>(ctx, a, 1, s);
-  return launch_cfg<WT, 1, RB, NMAT, 1, D>(ctx, a, 1, s);
+  if (nb >= 16) return launch_cfg<WT, 16, RB, NMAT, 1, D>(ctx, a, 1, s, e0, e1);
+  if (nb >= 8) return launch_cfg<WT, 8, RB, NMAT, 1, D>(ctx, a, 1, s, e0, e1);
+  if (nb >= 4) return launch_cfg<WT, 4, RB, NMAT, 1, D>(ctx, a, 1, s, e0, e1);
+  if (nb >= 2) return launch_cfg<WT, 2, RB, NMAT, 1, D>(ctx, a, 1, s, e0, e1);
+  return launch_cfg<WT, 1, RB, NMAT, 1, D>(ctx, a, 1, s, e0, e1);
 }
 
 template <int WT, int NMAT>
-int dispatch_shape(const tpt_ctx* ctx, const GemvArgs& a, hipStream_t s) {
-  if constexpr (NMAT == 2) return by_bpp<WT, 2, 1, 2>(ctx, a, s);
+int dispatch_shape(const tpt_ctx* ctx, const GemvArgs& a, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
+  if constexpr (NMAT == 2) return by_bpp<WT, 2, 1, 2>(ctx, a, s, e0, e1);
   else {
-    if (a.K > 8192) return by_bpp<WT, 1, 2, 2>(ctx, a, s);  // long rows: two rows per step
-    return by_bpp<WT, 1, 1, 2>(ctx, a, s);
+    if (a.K > 8192) return by_bpp<WT, 1, 2, 2>(ctx, a, s, e0, e1);  // long rows: two rows per step
+    return by_bpp<WT, 1, 1, 2>(ctx, a, s, e0, e1);
   }
 }
 
 }  // namespace
 
-int launch_gemv_q8(const tpt_ctx* ctx, int wtype, const GemvArgs& a, hipStream_t s) {
+int launch_gemv_q8(const tpt_ctx* ctx, int wtype, const GemvArgs& a, hipStream_t s, hipEvent_t ev0,
+                   hipEvent_t ev1) {
   if (a.K <= 0 || a.N <= 0 || a.K % 256) return fail(TPT_ERR_INVALID, "gemv: K must be a positive multiple of 256, N > 0");
   if (a.K > 64 * 256) return fail(TPT_ERR_UNSUPPORTED, "gemv: K > 16384 not supported");
   if (!a.w0 || !a.x) return fail(TPT_ERR_INVALID, "gemv: null weight/activation pointer");
@@ -733,9 +741,9 @@ int launch_gemv_q8(const tpt_ctx* ctx, int wtype, const GemvArgs& a, hipStream_t
     return fail(TPT_ERR_INVALID, "gemv: rope epilogue needs even row counts");
   const bool two = a.epilogue == EPI_SWIGLU;
   switch (wtype) {
-    case TPT_TYPE_Q4_K: return two ? dispatch_shape<TPT_TYPE_Q4_K, 2>(ctx, a, s) : dispatch_shape<TPT_TYPE_Q4_K, 1>(ctx, a, s);
-    case TPT_TYPE_Q6_K: return two ? dispatch_shape<TPT_TYPE_Q6_K, 2>(ctx, a, s) : dispatch_shape<TPT_TYPE_Q6_K, 1>(ctx, a, s);
-    case TPT_TYPE_Q8_0: return two ? dispatch_shape<TPT_TYPE_Q8_0, 2>(ctx, a, s) : dispatch_shape<TPT_TYPE_Q8_0, 1>(ctx, a, s);
+    case TPT_TYPE_Q4_K: return two ? dispatch_shape<TPT_TYPE_Q4_K, 2>(ctx, a, s, ev0, ev1) : dispatch_shape<TPT_TYPE_Q4_K, 1>(ctx, a, s, ev0, ev1);
+    case TPT_TYPE_Q6_K: return two ? dispatch_shape<TPT_TYPE_Q6_K, 2>(ctx, a, s, ev0, ev1) : dispatch_shape<TPT_TYPE_Q6_K, 1>(ctx, a, s, ev0, ev1);
+    case TPT_TYPE_Q8_0: return two ? dispatch_shape<TPT_TYPE_Q8_0, 2>(ctx, a, s, ev0, ev1) : dispatch_shape<TPT_TYPE_Q8_0, 1>(ctx, a, s, ev0, ev1);
   }
   return fail(TPT_ERR_UNSUPPORTED, "gemv: weight type must be Q4_K, Q6_K or Q8_0");
 }

@@ -50,8 +50,10 @@ struct GemvArgs {
   unsigned long long* amax = nullptr;  // slot array; slot = state ? amax[state->parity] : amax[0]
 };
 
-// Chooses the lane layout for K and launches.  wtype in {Q4_K, Q6_K, Q8_0}.
-int launch_gemv_q8(const tpt_ctx* ctx, int wtype, const GemvArgs& a, hipStream_t s);
+// Chooses the lane layout for K and launches.  wtype in {Q4_K, Q6_K, Q8_0}.  ev0/ev1, when
+// given, are timestamped by the dispatch itself (hipExtLaunchKernelGGL) around the kernel.
+int launch_gemv_q8(const tpt_ctx* ctx, int wtype, const GemvArgs& a, hipStream_t s,
+                   hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 int launch_gemv_f32(int wtype, const uint8_t* w, const float* x, float* y, int K, int N,
                     hipStream_t s);
 
