@@ -44,6 +44,7 @@ extern "C" {
  * times fp32 activations, fp32 accumulate. */
 #define TPT_ACT_Q8 0
 #define TPT_ACT_F32 1
+#define TPT_ACT_F16 2
 
 const char* tpt_last_error(void);
 int tpt_version(void);
@@ -78,6 +79,14 @@ int tpt_dequant(tpt_ctx* ctx, int type, const void* w, float* y, int64_t n);
  * dequant_and_gemm (wgpu_engine.rs:581-605) + gemm.wgsl:28-70 at M=1, and candle's
  * QMatMul::forward -> k_quants::matmul on the CPU (the parity target). */
 int tpt_gemv(tpt_ctx* ctx, int type, const void* w, const float* x, float* y, int K, int N,
+             int act_mode);
+
+/* Prefill GEMM on MFMA: Y[M,N] = X[M,K] . W[N,K]^T with W in Q4_K rows, X fp32 rows.
+ * act_mode TPT_ACT_Q8: every X row is quantized to Q8_K as candle's QMatMul does and the
+ * products are integer-exact (candle's prefill arithmetic); TPT_ACT_F16: X and the dequantized
+ * W in fp16 on the matrix cores, fp32 accumulate.  Replaces the per-position prefill of
+ * gpu_infer (wgpu_engine.rs:254-261) and candle's batched QMatMul (candle_engine.rs:272-273). */
+int tpt_gemm(tpt_ctx* ctx, int type, const void* w, const float* x, float* y, int M, int K, int N,
              int act_mode);
 
 /* y = rmsnorm(x) . W (fused norm prologue; the residual stream is normalised in-kernel).
@@ -115,6 +124,10 @@ int tpt_argmax(tpt_ctx* ctx, const float* logits, int64_t n, uint32_t* out_host)
  * interval between the start and stop events each dispatch timestamps itself. */
 int tpt_bench_gemv(tpt_ctx* ctx, int type, const void* const* weights, int n_weights,
                    const float* x, float* y, int K, int N, int iters, float* ms_out);
+/* iters launches of the GEMM kernel of tpt_gemm (activation rows prepared once, before the
+ * timed launches); *ms_out = the sum of the dispatch-stamped event intervals. */
+int tpt_bench_gemm(tpt_ctx* ctx, int type, const void* w, const float* x, float* y, int M, int K,
+                   int N, int act_mode, int iters, float* ms_out);
 /* iters launches of tpt_attn_decode over the same cache; *ms_out = total event time */
 int tpt_bench_attn(tpt_ctx* ctx, const float* q, const void* k_cache, const void* v_cache,
                    int kv_type, float* o, int nq, int nkv, int hd, int L, int L_stride,

@@ -242,3 +242,61 @@ def test_argmax_semantics(ctx):
     cases.append((big, 128000))
     for v, want in cases:
         assert ctx.argmax(ctx.to_device(v), v.size) == want == oracle.argmax(v)
+
+
+# ---------------------------------------------------------------- prefill GEMM (MFMA)
+
+def gemm_case(ctx, M, K, N, seed, bf16=False):
+    w = synth.random_weights(TYPE_Q4_K, N, K, seed=seed, name=f"g{K}x{N}")
+    x = np.random.default_rng(seed).standard_normal((M, K)).astype(np.float32)
+    if bf16:  # bf16 activations (values exactly representable in bf16)
+        x = (x.view(np.uint32) & 0xFFFF0000).view(np.float32)
+    return w, x
+
+
+@pytest.mark.parametrize("M,K,N", [(16, 256, 64), (33, 512, 300), (128, 4096, 4096), (200, 2048, 1000),
+                                   (130, 14336, 256)])
+def test_gemm_q8k_matches_candle(ctx, M, K, N):
+    """Q8_K mode: candle's prefill arithmetic (each X row quantized to Q8_K, integer dots);
+    the integer sums are exact, so only f32 block accumulation order differs."""
+    w, x = gemm_case(ctx, M, K, N, seed=M + K + N)
+    y = ctx.gemm(TYPE_Q4_K, ctx.to_device(w), ctx.to_device(x), M, K, N, act=tpthip.ACT_Q8)
+    rows = np.arange(M) if M * N <= 200 * 1000 else np.random.default_rng(0).choice(M, 24, replace=False)
+    ref = oracle.matmul(TYPE_Q4_K, x[rows], w, N)
+    for i, r in enumerate(rows):
+        assert rel_l2(y[r], ref[i]) < 1e-5, r
+
+
+def test_gemm_q8k_equals_gemv_rows(ctx):
+    """Batched prefill rows equal the decode GEMV of the same row (same Q8_K arithmetic)."""
+    M, K, N = 40, 4096, 512
+    w, x = gemm_case(ctx, M, K, N, seed=77)
+    wd = ctx.to_device(w)
+    y = ctx.gemm(TYPE_Q4_K, wd, ctx.to_device(x), M, K, N, act=tpthip.ACT_Q8)
+    for r in (0, 17, 39):
+        yv = ctx.gemv(TYPE_Q4_K, wd, ctx.to_device(x[r].copy()), K, N)
+        assert rel_l2(y[r], yv) < 1e-6
+
+
+@pytest.mark.parametrize("M,N", [(128, 4096), (512, 4096), (2048, 4096), (128, 14336), (512, 14336),
+                                 (2048, 14336)])
+def test_gemm_f16_config3(ctx, M, N):
+    """fp16 MFMA mode at the prefill shapes (K=4096, bf16 activations): within 1e-3 relative L2
+    of the fp64 product of the exactly dequantized weights (checked on a row/column sample)."""
+    K = 4096
+    w, x = gemm_case(ctx, M, K, N, seed=M * 3 + N, bf16=True)
+    y = ctx.gemm(TYPE_Q4_K, ctx.to_device(w), ctx.to_device(x), M, K, N, act=tpthip.ACT_F16)
+    nc = min(N, 1024)
+    wdq = oracle.dequant(TYPE_Q4_K, w[: nc * (K // 256) * 144], nc * K).astype(np.float64).reshape(nc, K)
+    rows = np.random.default_rng(1).choice(M, min(M, 64), replace=False)
+    ref = x[rows].astype(np.float64) @ wdq.T
+    assert rel_l2(y[rows][:, :nc], ref) < 1e-3
+
+
+def test_gemm_rejects_bad_shapes(ctx):
+    w = ctx.alloc(4096)
+    x = ctx.alloc(4096)
+    with pytest.raises(tpthip.TptError):
+        ctx.gemm(TYPE_Q4_K, w, x, 4, 100, 4, act=tpthip.ACT_Q8)  # K not a multiple of 256
+    with pytest.raises(tpthip.TptError):
+        ctx.gemm(TYPE_Q6_K, w, x, 4, 256, 4, act=tpthip.ACT_Q8)  # only Q4_K on the MFMA path

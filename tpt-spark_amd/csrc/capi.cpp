@@ -265,6 +265,85 @@ int tpt_argmax(tpt_ctx* c, const float* logits, int64_t n, uint32_t* out_host) {
   return rc;
 }
 
+namespace {
+// Device scratch for one tpt_gemm / tpt_bench_gemm call: the prepared activation rows.
+struct GemmCall {
+  GemmArgs g;
+  void* scratch = nullptr;
+};
+int gemm_prepare(tpt_ctx* c, int type, const void* w, const float* x, float* y, int M, int K,
+                 int N, int act_mode, GemmCall* call) {
+  if (type != TPT_TYPE_Q4_K) return fail(TPT_ERR_UNSUPPORTED, "gemm: weight type must be Q4_K");
+  if (act_mode != TPT_ACT_Q8 && act_mode != TPT_ACT_F16) return fail(TPT_ERR_INVALID, "gemm: act_mode must be TPT_ACT_Q8 or TPT_ACT_F16");
+  if (!w || !x || !y || M <= 0 || N <= 0 || K <= 0 || K % 256) return fail(TPT_ERR_INVALID, "gemm: bad arguments");
+  GemmArgs& g = call->g;
+  g.M = M; g.N = N; g.K = K;
+  g.mode = act_mode == TPT_ACT_Q8 ? GEMM_Q8K : GEMM_F16;
+  g.w = (const uint8_t*)w;
+  g.w_stride = row_bytes(type, K);
+  g.y = y;
+  g.ldy = N;
+  ActPrepArgs p;
+  p.M = M; p.K = K; p.ldx = K; p.x = x; p.mode = g.mode;
+  const size_t mk = (size_t)M * K;
+  const size_t bytes = g.mode == GEMM_Q8K ? mk + (size_t)M * (K / 256) * 4 + (size_t)M * (K / 16) * 2 + 512 : mk * 2 + 256;
+  TPT_HIP(hipMallocAsync(&call->scratch, bytes, c->stream));
+  uint8_t* base = (uint8_t*)call->scratch;
+  if (g.mode == GEMM_Q8K) {
+    p.aq = (int8_t*)base;
+    p.ad = (float*)(base + ((mk + 255) & ~(size_t)255));
+    p.as16 = (int16_t*)(base + ((mk + 255) & ~(size_t)255) + (((size_t)M * (K / 256) * 4 + 255) & ~(size_t)255));
+    g.aq = p.aq; g.ad = p.ad; g.as16 = p.as16;
+  } else {
+    p.af = (uint16_t*)base;
+    g.af = p.af;
+  }
+  int rc = launch_act_prep(p, c->stream);
+  if (rc) (void)hipFreeAsync(call->scratch, c->stream);
+  return rc;
+}
+}  // namespace
+
+int tpt_gemm(tpt_ctx* c, int type, const void* w, const float* x, float* y, int M, int K, int N,
+             int act_mode) {
+  ENTER(c);
+  GemmCall call;
+  int rc = gemm_prepare(c, type, w, x, y, M, K, N, act_mode, &call);
+  if (rc) return rc;
+  rc = launch_gemm_q4k(call.g, c->stream);
+  (void)hipFreeAsync(call.scratch, c->stream);
+  return rc;
+}
+
+int tpt_bench_gemm(tpt_ctx* c, int type, const void* w, const float* x, float* y, int M, int K,
+                   int N, int act_mode, int iters, float* ms_out) {
+  ENTER(c);
+  if (iters <= 0 || iters > 4096 || !ms_out) return fail(TPT_ERR_INVALID, "bench_gemm: bad arguments");
+  GemmCall call;
+  int rc = gemm_prepare(c, type, w, x, y, M, K, N, act_mode, &call);
+  if (rc) return rc;
+  std::vector<hipEvent_t> ev((size_t)2 * iters, nullptr);
+  hipError_t e = hipSuccess;
+  for (auto& v : ev)
+    if (e == hipSuccess) e = hipEventCreate(&v);
+  for (int i = 0; i < iters && rc == TPT_OK && e == hipSuccess; i++)
+    rc = launch_gemm_q4k_timed(call.g, c->stream, ev[2 * i], ev[2 * i + 1]);
+  if (e == hipSuccess && rc == TPT_OK) e = hipEventSynchronize(ev.back());
+  float total = 0.f;
+  for (int i = 0; i < iters && e == hipSuccess && rc == TPT_OK; i++) {
+    float ms = 0.f;
+    e = hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]);
+    total += ms;
+  }
+  for (auto& v : ev)
+    if (v) (void)hipEventDestroy(v);
+  (void)hipFreeAsync(call.scratch, c->stream);
+  if (rc) return rc;
+  if (e != hipSuccess) return hip_fail(e, "bench_gemm", __FILE__, __LINE__);
+  *ms_out = total;
+  return TPT_OK;
+}
+
 int tpt_bench_gemv(tpt_ctx* c, int type, const void* const* weights, int n_weights,
                    const float* x, float* y, int K, int N, int iters, float* ms_out) {
   ENTER(c);

@@ -96,13 +96,13 @@ __global__ void __launch_bounds__(ANT) attn_partial_kernel(const AttnArgs a, con
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int li = tid % LPP, pg = tid / LPP;  // lane in position, position group 0..R-1
-  const int kvh = blockIdx.y, chunk = blockIdx.x, nch = gridDim.x;
+  const int kvh = blockIdx.y, chunk = blockIdx.x, nch = gridDim.x, t = blockIdx.z;
   // The chunk's rows are known at launch; the live length L (from the step state on the
   // decode path) only masks, so the K/V loads do not wait for it.
   const int CL = a.chunk_len;
   const int p0 = chunk * CL;
   const int plast = min(p0 + CL, a.L_stride) - 1;  // clamped loads stay inside the cache
-  const int L = a.state ? a.state->pos + 1 : a.L_host;
+  const int L = (a.state ? a.state->pos + 1 : a.L_host) + t;
   const int p1 = min(L, p0 + CL);
   const int n = p1 - p0;  // may be <= 0 for trailing chunks
 
@@ -113,7 +113,7 @@ __global__ void __launch_bounds__(ANT) attn_partial_kernel(const AttnArgs a, con
 #pragma unroll
   for (int h = 0; h < G; h++)
 #pragma unroll
-    for (int e = 0; e < EPL; e++) q[h][e] = a.q[(size_t)(kvh * G + h) * HD + li * EPL + e];
+    for (int e = 0; e < EPL; e++) q[h][e] = a.q[(size_t)t * a.ldq + (size_t)(kvh * G + h) * HD + li * EPL + e];
 
   // phase 1: scores (the first round also fetches its V rows)
   float vpre[U][EPL];
@@ -224,7 +224,7 @@ __global__ void __launch_bounds__(ANT) attn_partial_kernel(const AttnArgs a, con
     for (int e = 0; e < EPL; e++) s_o[pg][h][li * EPL + e] = o[h][e];
   __syncthreads();
 
-  float* part = a.part + ((size_t)kvh * nch + chunk) * G * PSTRIDE;
+  float* part = a.part + (((size_t)t * gridDim.y + kvh) * nch + chunk) * G * PSTRIDE;
   for (int i = tid; i < G * HD; i += ANT) {
     const int h = i / HD, d = i % HD;
     float s = 0.f;
@@ -242,16 +242,18 @@ __global__ void __launch_bounds__(ANT) attn_partial_kernel(const AttnArgs a, con
 // 32 consecutive output dims of one head; thread (set, j) sums chunks set, set + 8, ...
 template <int HD, int G>
 __global__ void __launch_bounds__(ANT) attn_merge_kernel(const float* __restrict__ part,
-                                                         float* __restrict__ out, int nch) {
+                                                         float* __restrict__ out, int nch, int ldo) {
   constexpr int PSTRIDE = HD + 2;
   constexpr int TILES = G * HD / MT;  // merge workgroups per kv head
   __shared__ float s_w[NCH_MAX];
   __shared__ float s_acc[MSETS][MT];
   __shared__ float s_l;
   const int tid = threadIdx.x, lane = tid & 63;
-  const int kvh = blockIdx.x / TILES, d0 = (blockIdx.x % TILES) * MT;
+  const int kvh = blockIdx.x / TILES, d0 = (blockIdx.x % TILES) * MT, t = blockIdx.y;
+  const int nkv = gridDim.x / TILES;
   const int h = d0 / HD, dh = d0 % HD;
-  const float* pk = part + (size_t)kvh * nch * G * PSTRIDE + (size_t)h * PSTRIDE;
+  out += (size_t)t * ldo;
+  const float* pk = part + ((size_t)t * nkv + kvh) * nch * G * PSTRIDE + (size_t)h * PSTRIDE;
   const int j = tid % MT, set = tid / MT;
   const float* src = pk + dh + j;
   // first 8 chunks of this thread's set, issued before the weights (clamped: always in bounds)
@@ -300,15 +302,15 @@ __global__ void __launch_bounds__(ANT) attn_merge_kernel(const float* __restrict
 
 template <typename T, int HD, int G>
 int launch_g(const AttnArgs& a, float scale, hipStream_t s) {
-  const dim3 grid((unsigned)a.n_chunks, (unsigned)a.nkv);
+  const dim3 grid((unsigned)a.n_chunks, (unsigned)a.nkv, (unsigned)a.nqb);
   constexpr int R = ANT / KvTraits<T>::LPP;
   if (a.chunk_len <= 4 * R)
     hipLaunchKernelGGL((attn_partial_kernel<T, HD, G, 4>), grid, dim3(ANT), 0, s, a, scale);
   else
     hipLaunchKernelGGL((attn_partial_kernel<T, HD, G, 8>), grid, dim3(ANT), 0, s, a, scale);
   TPT_HIP(hipGetLastError());
-  hipLaunchKernelGGL((attn_merge_kernel<HD, G>), dim3((unsigned)(a.nkv * G * HD / MT)), dim3(ANT), 0,
-                     s, (const float*)a.part, a.o, a.n_chunks);
+  hipLaunchKernelGGL((attn_merge_kernel<HD, G>), dim3((unsigned)(a.nkv * G * HD / MT), (unsigned)a.nqb),
+                     dim3(ANT), 0, s, (const float*)a.part, a.o, a.n_chunks, a.ldo);
   TPT_HIP(hipGetLastError());
   return TPT_OK;
 }
@@ -369,6 +371,12 @@ int launch_attn_decode(const AttnArgs& a, hipStream_t s) {
     return fail(TPT_ERR_INVALID, "attention: chunk length must be a multiple of 16 in [16, 1024]");
   if (!a.state && (long)a.chunk_len * a.n_chunks < a.L_host)
     return fail(TPT_ERR_INVALID, "attention: chunks do not cover the length");
+  if (a.nqb < 1 || (a.nqb > 1 && (a.state || a.ldq < a.nq * a.hd || a.ldo < a.nq * a.hd)))
+    return fail(TPT_ERR_INVALID, "attention: bad query batch");
+  if (!a.state && a.L_host + a.nqb - 1 > a.L_stride)
+    return fail(TPT_ERR_INVALID, "attention: queries past the cache");
+  if (!a.state && (long)a.chunk_len * a.n_chunks < a.L_host + a.nqb - 1)
+    return fail(TPT_ERR_INVALID, "attention: chunks do not cover the last query");
   if (a.kv_type != TPT_TYPE_F16 && a.kv_type != TPT_TYPE_F32)
     return fail(TPT_ERR_UNSUPPORTED, "attention: KV cache type must be F16 or F32");
   const float scale = (float)(1.0 / __builtin_sqrt((double)a.hd));

@@ -194,33 +194,10 @@ __device__ void prologue_q8k(const GemvArgs& A, const XPre& p, const Lds& L) {
     if (b < nb) {
       const float4 v = norm ? apply_norm(p.x[i], p.w[i], m) : p.x[i];
       const float e[4] = {v.x, v.y, v.z, v.w};
-      // the signed value of largest |x|, first occurrence winning ties: the max of |x| over
-      // the wave, then the first lane (and its first element) holding it
-      const float la = fmaxf(fmaxf(fabsf(e[0]), fabsf(e[1])), fmaxf(fabsf(e[2]), fabsf(e[3])));
-      const float amax = wave_max_dpp(la);
-      const float mine = fabsf(e[0]) == amax ? e[0] : fabsf(e[1]) == amax ? e[1]
-                         : fabsf(e[2]) == amax ? e[2] : e[3];
-      const unsigned long long hit = __ballot(la == amax);
-      const int first = hit ? (int)__builtin_ctzll(hit) : 0;
-      const float mx = readlane_f(mine, first);
-      int packed = 0, qsum = 0;
-      float d = 0.f;
-      if (amax != 0.f) {
-        const float iscale = -128.f / mx;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          float r = roundf(iscale * e[j]);
-          r = fminf(r, 127.f);
-          r = fmaxf(r, -128.f);
-          const int q = (int)r;
-          qsum += q;
-          packed |= (q & 0xff) << (8 * j);
-        }
-        d = 1.f / iscale;
-      }
+      int qsum;
+      float d;
+      const int packed = q8k_block_wave(e, &qsum, &d);
       L.q32[b * 64 + lane] = packed;
-      qsum += dpp_i<0xB1>(qsum);  // sums of 16 values: groups of 4 lanes
-      qsum += dpp_i<0x4E>(qsum);
       if ((lane & 3) == 0) L.s16[b * 16 + (lane >> 2)] = qsum;
       if (lane == 0) L.d[b] = d;
     }

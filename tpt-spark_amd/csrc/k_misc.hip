@@ -92,6 +92,52 @@ __global__ void __launch_bounds__(256) step_begin_kernel(StepState* st, const ui
   }
 }
 
+// Embedding rows of T token ids (prefill): x[t] = dequant(embd[ids[t]]), one workgroup per row.
+__global__ void __launch_bounds__(256) embed_rows_kernel(const uint32_t* ids, int embd_type,
+                                                         const uint8_t* embd, size_t embd_row_bytes,
+                                                         int H, float* x) {
+  const int t = blockIdx.x;
+  const uint8_t* row = embd + (size_t)ids[t] * embd_row_bytes;
+  for (int i = threadIdx.x; i < H; i += blockDim.x) x[(size_t)t * H + i] = dequant_elem(embd_type, row, i);
+}
+
+// Q/K/V post-pass of the prefill: one thread per (even, odd) element pair of a row.  RoPE as
+// candle's rope_i (dst[2i] = x0*cos - x1*sin; dst[2i+1] = x0*sin + x1*cos) at the row's position,
+// the same arithmetic as the decode GEMV's epilogue.
+__global__ void __launch_bounds__(256) qkv_post_kernel(const QkvPostArgs a) {
+  const int t = blockIdx.y, pos = a.pos0 + t;
+  const int npair = (a.qd + 2 * a.kd) / 2;
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= npair) return;
+  const int e = 2 * p;
+  const float* row = a.qkv + (size_t)t * (a.qd + 2 * a.kd);
+  const float x0 = row[e], x1 = row[e + 1];
+  float o0 = x0, o1 = x1;
+  if (e < a.qd + a.kd) {
+    const int rr = e < a.qd ? e : e - a.qd;
+    const size_t ti = (size_t)pos * (a.hd / 2) + ((rr % a.hd) >> 1);
+    const float cs = a.rope_cos[ti], sn = a.rope_sin[ti];
+    o0 = x0 * cs - x1 * sn;
+    o1 = x0 * sn + x1 * cs;
+  }
+  if (e < a.qd) {
+    a.q[(size_t)t * a.qd + e] = o0;
+    a.q[(size_t)t * a.qd + e + 1] = o1;
+    return;
+  }
+  const bool isk = e < a.qd + a.kd;
+  const int rr = isk ? e - a.qd : e - a.qd - a.kd;
+  const size_t ci = ((size_t)(rr / a.hd) * a.max_ctx + pos) * a.hd + rr % a.hd;
+  void* cache = isk ? a.kcache : a.vcache;
+  if (a.kv_type == TPT_TYPE_F32) {
+    ((float*)cache)[ci] = o0;
+    ((float*)cache)[ci + 1] = o1;
+  } else {
+    ((uint16_t*)cache)[ci] = f2h(o0);
+    ((uint16_t*)cache)[ci + 1] = f2h(o1);
+  }
+}
+
 // candle_nn::ops::rms_norm: m = sqrt(sum(x^2)/n + eps); y = x / m * w (one workgroup)
 __global__ void __launch_bounds__(1024) rmsnorm_kernel(const float* __restrict__ x,
                                                        const float* __restrict__ w,
@@ -177,6 +223,25 @@ int launch_step_begin(StepState* st, const uint32_t* prompt, int embd_type, cons
     return fail(TPT_ERR_UNSUPPORTED, "embedding rows must be of even length and at most 64 KB");
   hipLaunchKernelGGL(step_begin_kernel, dim3(1), dim3(256), embd_row_bytes, s, st, prompt,
                      embd_type, embd, embd_row_bytes, H, vocab, x, tok_log);
+  TPT_HIP(hipGetLastError());
+  return TPT_OK;
+}
+
+int launch_embed_rows(const uint32_t* ids, int T, int embd_type, const uint8_t* embd,
+                      size_t embd_row_bytes, int H, float* x, hipStream_t s) {
+  if (T <= 0 || H <= 0) return fail(TPT_ERR_INVALID, "embed_rows: bad shape");
+  hipLaunchKernelGGL(embed_rows_kernel, dim3((unsigned)T), dim3(256), 0, s, ids, embd_type, embd,
+                     embd_row_bytes, H, x);
+  TPT_HIP(hipGetLastError());
+  return TPT_OK;
+}
+
+int launch_qkv_post(const QkvPostArgs& a, hipStream_t s) {
+  if (a.T <= 0 || a.qd <= 0 || a.kd <= 0 || a.hd <= 0 || (a.hd & 1) || a.qd % a.hd || a.kd % a.hd)
+    return fail(TPT_ERR_INVALID, "qkv_post: bad shape");
+  if (a.pos0 < 0 || a.pos0 + a.T > a.max_ctx) return fail(TPT_ERR_INVALID, "qkv_post: positions past the cache");
+  const int npair = (a.qd + 2 * a.kd) / 2;
+  hipLaunchKernelGGL(qkv_post_kernel, dim3((unsigned)((npair + 255) / 256), (unsigned)a.T), dim3(256), 0, s, a);
   TPT_HIP(hipGetLastError());
   return TPT_OK;
 }

@@ -57,6 +57,41 @@ int launch_gemv_q8(const tpt_ctx* ctx, int wtype, const GemvArgs& a, hipStream_t
 int launch_gemv_f32(int wtype, const uint8_t* w, const float* x, float* y, int K, int N,
                     hipStream_t s);
 
+// ---- prefill GEMM (k_gemm.hip): Y[M,N] = X[M,K] . W[N,K]^T, W in Q4_K blocks
+enum GemmMode { GEMM_Q8K = 0, GEMM_F16 = 1 };
+struct GemmArgs {
+  int M = 0, N = 0, K = 0, mode = GEMM_Q8K;
+  const uint8_t* w = nullptr;
+  size_t w_stride = 0;               // bytes per weight row
+  const int8_t* aq = nullptr;        // GEMM_Q8K: [M][K] int8
+  const float* ad = nullptr;         //           [M][K/256] block scales
+  const int16_t* as16 = nullptr;     //           [M][K/16] per-16 sums
+  const uint16_t* af = nullptr;      // GEMM_F16: [M][K] fp16 bits
+  float* y = nullptr;
+  int ldy = 0;
+  const float* resid = nullptr;      // optional: y = X.W^T + resid
+  int ldr = 0;
+};
+int launch_gemm_q4k(const GemmArgs& g, hipStream_t s);
+// the same launch with dispatch-stamped start/stop events (hipExtLaunchKernelGGL)
+int launch_gemm_q4k_timed(const GemmArgs& g, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1);
+
+// Activation rows for the prefill GEMM: optional RMSNorm (w, eps) or SwiGLU (silu(x) * x2),
+// then Q8_K quantization (aq/ad/as16) or fp16 conversion (af).  x rows of K floats, stride ldx.
+struct ActPrepArgs {
+  int M = 0, K = 0, ldx = 0;
+  const float* x = nullptr;
+  const float* x2 = nullptr;         // SwiGLU: up values (same layout as x = gate)
+  const float* norm_w = nullptr;     // RMSNorm weights (nullptr: no norm)
+  float eps = 0.f;
+  int mode = GEMM_Q8K;
+  int8_t* aq = nullptr;
+  float* ad = nullptr;
+  int16_t* as16 = nullptr;
+  uint16_t* af = nullptr;
+};
+int launch_act_prep(const ActPrepArgs& a, hipStream_t s);
+
 int launch_dequant(int type, const void* w, float* y, int64_t n, hipStream_t s);
 int launch_rmsnorm(const float* x, const float* w, float* y, int n, float eps, hipStream_t s);
 int launch_rope(float* x, int n_heads, int hd, int pos, const float* c, const float* sn,
@@ -76,7 +111,10 @@ struct AttnArgs {
   int n_chunks = 0;
   int chunk_len = 0;                 // positions per chunk (multiple of 16, <= 1024); chunk c
                                      // covers [c*chunk_len, (c+1)*chunk_len) clipped to L
-  float* part = nullptr;             // [nkv][n_chunks][G][hd + 2] chunk records
+  float* part = nullptr;             // [nqb][nkv][n_chunks][G][hd + 2] chunk records
+  // prefill: nqb query positions at once; query t reads q + t*ldq, writes o + t*ldo and sees
+  // L + t cached positions (causal)
+  int nqb = 1, ldq = 0, ldo = 0;
 };
 int attn_part_floats(int nq, int nkv, int hd, int n_chunks);
 int attn_default_chunks(int L, int nkv);
@@ -86,6 +124,22 @@ int launch_attn_decode(const AttnArgs& a, hipStream_t s);
 
 // Start of a decode step: pick the token, embed it (x = dequant(token_embd[tok])), advance the
 // step state and clear the amax slot the LM head will write.
+// Prefill helpers: embedding rows of T token ids, and the Q/K/V post-pass (interleaved RoPE of
+// q and k at positions pos0 + t, q to q_out [T][qd], k and v appended to the cache).
+int launch_embed_rows(const uint32_t* ids, int T, int embd_type, const uint8_t* embd,
+                      size_t embd_row_bytes, int H, float* x, hipStream_t s);
+struct QkvPostArgs {
+  const float* qkv = nullptr;  // [T][qd + 2kd]
+  int T = 0, qd = 0, kd = 0, hd = 0;
+  float* q = nullptr;          // [T][qd]
+  void* kcache = nullptr;
+  void* vcache = nullptr;
+  int kv_type = TPT_TYPE_F16, max_ctx = 0, pos0 = 0;
+  const float* rope_cos = nullptr;
+  const float* rope_sin = nullptr;
+};
+int launch_qkv_post(const QkvPostArgs& a, hipStream_t s);
+
 int launch_step_begin(StepState* st, const uint32_t* prompt, int embd_type,
                       const uint8_t* embd, size_t embd_row_bytes, int H, int vocab, float* x,
                       uint32_t* tok_log, hipStream_t s);

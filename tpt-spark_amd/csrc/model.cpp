@@ -49,6 +49,7 @@ tpt_model::~tpt_model() {
   graphs.clear();
   if (arena) (void)hipFree(arena);
   if (runtime) (void)hipFree(runtime);
+  if (pf_mem) (void)hipFree(pf_mem);
   if (st_host) (void)hipHostFree(st_host);
   if (ids_host) (void)hipHostFree(ids_host);
 }
@@ -288,6 +289,12 @@ int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_t
   }
   TPT_HIP(hipHostMalloc((void**)&st_host, sizeof(StepState)));
   TPT_HIP(hipHostMalloc((void**)&ids_host, (size_t)max_ctx * 4));
+  batched_prefill = true;
+  for (const Layer& L : layers)
+    for (int t : {L.tq, L.tk, L.tv, L.to, L.tg, L.tu, L.td})
+      if (t != TPT_TYPE_Q4_K) batched_prefill = false;
+  const char* ev_pf = getenv("TPT_HIP_PREFILL");
+  if (ev_pf && strcmp(ev_pf, "steps") == 0) batched_prefill = false;
   const char* ev_graph = getenv("TPT_HIP_GRAPHS");
   use_graphs = !(ev_graph && ev_graph[0] == '0');
   TPT_HIP(hipStreamSynchronize(stream));
@@ -465,16 +472,150 @@ int tpt_model::read_state(StepState* out_state) {
   return TPT_OK;
 }
 
+int tpt_model::prefill_steps(int n, int pos0) {
+  int rc = set_state(pos0, pos0 + n, 0, 0);
+  if (rc) return rc;
+  for (int i = 0; i < n; i++)
+    if ((rc = launch_step(pos0 + i + 1, true))) return rc;
+  return TPT_OK;
+}
+
+int tpt_model::prefill_scratch(int T, int n_chunks) {
+  const int H = desc.embed, qd = desc.n_heads * desc.head_dim, kd = desc.n_kv_heads * desc.head_dim;
+  const int F = desc.ffn, Kmax = std::max(std::max(H, qd), F);
+  size_t off = 0;
+  auto carve = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes, 256); return o; };
+  const size_t o_x = carve((size_t)T * H * 4), o_aq = carve((size_t)T * Kmax),
+               o_ad = carve((size_t)T * (Kmax / 256) * 4), o_as = carve((size_t)T * (Kmax / 16) * 2),
+               o_qkv = carve((size_t)T * (qd + 2 * kd) * 4), o_q = carve((size_t)T * qd * 4),
+               o_att = carve((size_t)T * qd * 4), o_g = carve((size_t)T * F * 4), o_u = carve((size_t)T * F * 4),
+               o_part = carve((size_t)T * attn_part_floats(desc.n_heads, desc.n_kv_heads, desc.head_dim, n_chunks) * 4),
+               o_ids = carve((size_t)T * 4);
+  if (off > pf_bytes) {
+    if (pf_mem) {
+      TPT_HIP(hipStreamSynchronize(stream));
+      TPT_HIP(hipFree(pf_mem));
+      pf_mem = nullptr;
+      pf_bytes = 0;
+    }
+    TPT_HIP(hipMalloc(&pf_mem, off));
+    pf_bytes = off;
+  }
+  uint8_t* b = (uint8_t*)pf_mem;
+  pf_x = (float*)(b + o_x);
+  pf_aq = (int8_t*)(b + o_aq);
+  pf_ad = (float*)(b + o_ad);
+  pf_as16 = (int16_t*)(b + o_as);
+  pf_qkv = (float*)(b + o_qkv);
+  pf_q = (float*)(b + o_q);
+  pf_att = (float*)(b + o_att);
+  pf_g = (float*)(b + o_g);
+  pf_u = (float*)(b + o_u);
+  pf_part = (float*)(b + o_part);
+  pf_ids = (uint32_t*)(b + o_ids);
+  return TPT_OK;
+}
+
+// Batched prefill of positions pos0 .. pos0+n-1 (ids in ids_host[pos0 ..]): slices of up to
+// kPrefillT positions run the whole layer stack as GEMMs (candle's batched forward,
+// candle_engine.rs:272-273: per layer rms_norm, Q/K/V, rope_i, KV append, causal attention,
+// Wo + residual, rms_norm, SwiGLU, down + residual), leaving the last position's residual
+// stream in x for the LM head.
+int tpt_model::prefill_batched(int n, int pos0) {
+  const int H = desc.embed, hd = desc.head_dim, nq = desc.n_heads, nkv = desc.n_kv_heads;
+  const int qd = nq * hd, kd = nkv * hd, F = desc.ffn, mc = desc.max_ctx;
+  const size_t layer_kv = (size_t)2 * nkv * mc * hd;
+  int rc;
+  for (int c0 = 0; c0 < n; c0 += kPrefillT) {
+    const int T = std::min(kPrefillT, n - c0), p0 = pos0 + c0;
+    const int Lmax = p0 + T;
+    int nch = (Lmax + 511) / 512;
+    const int cl = attn_chunk_len(Lmax, nch);
+    if ((rc = prefill_scratch(T, nch))) return rc;
+    TPT_HIP(hipMemcpyAsync(pf_ids, ids_host + p0, (size_t)T * 4, hipMemcpyHostToDevice, stream));
+    if ((rc = launch_embed_rows(pf_ids, T, embd_type, embd, embd_row, H, pf_x, stream))) return rc;
+    auto prep = [&](const float* x, const float* x2, int K, const float* nw) {
+      ActPrepArgs a;
+      a.M = T; a.K = K; a.ldx = K; a.x = x; a.x2 = x2; a.norm_w = nw; a.eps = desc.rms_eps;
+      a.mode = GEMM_Q8K; a.aq = pf_aq; a.ad = pf_ad; a.as16 = pf_as16;
+      return launch_act_prep(a, stream);
+    };
+    auto gemm = [&](const uint8_t* w, int K, int N, float* y, int ldy, const float* resid) {
+      GemmArgs g;
+      g.M = T; g.N = N; g.K = K; g.mode = GEMM_Q8K;
+      g.w = w; g.w_stride = row_bytes(TPT_TYPE_Q4_K, K);
+      g.aq = pf_aq; g.ad = pf_ad; g.as16 = pf_as16;
+      g.y = y; g.ldy = ldy; g.resid = resid; g.ldr = ldy;
+      return launch_gemm_q4k(g, stream);
+    };
+    for (int l = 0; l < desc.n_layers; l++) {
+      const Layer& L = layers[l];
+      uint8_t* kc = (uint8_t*)kv + (size_t)l * layer_kv * kv_elem;
+      uint8_t* vc = kc + (size_t)nkv * mc * hd * kv_elem;
+      if ((rc = prep(pf_x, nullptr, H, L.attn_norm))) return rc;
+      const int ldq = qd + 2 * kd;
+      if (L.qkv_adjacent) {
+        if ((rc = gemm(L.q, H, ldq, pf_qkv, ldq, nullptr))) return rc;
+      } else {
+        if ((rc = gemm(L.q, H, qd, pf_qkv, ldq, nullptr)) || (rc = gemm(L.k, H, kd, pf_qkv + qd, ldq, nullptr)) ||
+            (rc = gemm(L.v, H, kd, pf_qkv + qd + kd, ldq, nullptr)))
+          return rc;
+      }
+      QkvPostArgs qp;
+      qp.qkv = pf_qkv; qp.T = T; qp.qd = qd; qp.kd = kd; qp.hd = hd; qp.q = pf_q;
+      qp.kcache = kc; qp.vcache = vc; qp.kv_type = desc.kv_type; qp.max_ctx = mc; qp.pos0 = p0;
+      qp.rope_cos = rope_cos; qp.rope_sin = rope_sin;
+      if ((rc = launch_qkv_post(qp, stream))) return rc;
+      AttnArgs at;
+      at.q = pf_q; at.ldq = qd; at.kc = kc; at.vc = vc; at.kv_type = desc.kv_type;
+      at.o = pf_att; at.ldo = qd; at.nq = nq; at.nkv = nkv; at.hd = hd; at.L_stride = mc;
+      at.L_host = p0 + 1; at.nqb = T; at.n_chunks = nch; at.chunk_len = cl; at.part = pf_part;
+      if ((rc = launch_attn_decode(at, stream))) return rc;
+      if ((rc = prep(pf_att, nullptr, qd, nullptr)) || (rc = gemm(L.o, qd, H, pf_x, H, pf_x))) return rc;
+      if ((rc = prep(pf_x, nullptr, H, L.ffn_norm)) || (rc = gemm(L.gate, H, F, pf_g, F, nullptr)) ||
+          (rc = gemm(L.up, H, F, pf_u, F, nullptr)))
+        return rc;
+      if ((rc = prep(pf_g, pf_u, F, nullptr)) || (rc = gemm(L.down, F, H, pf_x, H, pf_x))) return rc;
+    }
+    // the last position's residual stream feeds the LM head
+    TPT_HIP(hipMemcpyAsync(x, pf_x + (size_t)(T - 1) * H, (size_t)H * 4, hipMemcpyDeviceToDevice, stream));
+  }
+  return TPT_OK;
+}
+
 int tpt_model::prefill(const uint32_t* ids, int n, int pos0, uint32_t* next_out, float* logits_out) {
   if (n <= 0 || pos0 < 0 || pos0 + n > desc.max_ctx) return fail(TPT_ERR_INVALID, "prefill: positions out of range");
   for (int i = 0; i < n; i++)
     if (ids[i] >= (uint32_t)desc.vocab) return fail(TPT_ERR_INVALID, "prefill: token id out of vocabulary");
   memcpy(ids_host + pos0, ids, (size_t)n * 4);
   TPT_HIP(hipMemcpyAsync(prompt_dev + pos0, ids_host + pos0, (size_t)n * 4, hipMemcpyHostToDevice, stream));
-  int rc = set_state(pos0, pos0 + n, 0, 0);
-  if (rc) return rc;
-  for (int i = 0; i < n; i++)
-    if ((rc = launch_step(pos0 + i + 1, true))) return rc;
+  int rc;
+  if (batched_prefill && n >= 2) {
+    if ((rc = prefill_batched(n, pos0))) return rc;
+    // LM head + greedy token of the last position, with the step state pointing at it
+    memset(st_host, 0, sizeof(StepState));
+    st_host->pos = pos0 + n - 1;
+    st_host->next_pos = pos0 + n;
+    st_host->prompt_len = pos0 + n;
+    TPT_HIP(hipMemcpyAsync(st, st_host, sizeof(StepState), hipMemcpyHostToDevice, stream));
+    TPT_HIP(hipStreamSynchronize(stream));  // the pinned source must not change before the copy
+    GemvArgs lh;
+    lh.w0 = out;
+    lh.row_stride = row_bytes(out_type, desc.embed);
+    lh.K = desc.embed;
+    lh.N = desc.vocab;
+    lh.x = x;
+    lh.norm_w = out_norm;
+    lh.eps = desc.rms_eps;
+    lh.prologue = PRO_RMSNORM;
+    lh.epilogue = EPI_ARGMAX;
+    lh.y = logits;
+    lh.amax = (unsigned long long*)((char*)st + offsetof(StepState, amax));
+    lh.state = st;
+    if ((rc = launch_gemv_q8(ctx, out_type, lh, stream))) return rc;
+  } else if ((rc = prefill_steps(n, pos0))) {
+    return rc;
+  }
   StepState s;
   if ((rc = read_state(&s))) return rc;
   if (next_out) *next_out = (uint32_t)(s.amax[s.parity] & 0xffffffffull);

@@ -49,6 +49,17 @@ struct tpt_model {
   bool use_graphs = true;
   std::map<int, hipGraphExec_t> graphs;  // by length bucket
 
+  // batched prefill (MFMA GEMMs over up to kPrefillT positions at once)
+  static constexpr int kPrefillT = 1024;
+  bool batched_prefill = false;       // every layer matrix is Q4_K
+  void* pf_mem = nullptr;             // scratch of the batched prefill, grown on demand
+  size_t pf_bytes = 0;
+  float *pf_x = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_att = nullptr, *pf_g = nullptr,
+        *pf_u = nullptr, *pf_part = nullptr, *pf_ad = nullptr;
+  int8_t* pf_aq = nullptr;
+  int16_t* pf_as16 = nullptr;
+  uint32_t* pf_ids = nullptr;
+
   ~tpt_model();
   int load(tpt_ctx* c, const char* gguf_path, int max_ctx, int kv_type, tpt_progress_fn progress,
            void* user);
@@ -58,6 +69,9 @@ struct tpt_model {
   int set_state(int next_pos, int prompt_len, int use_override, uint32_t tok);
   int read_state(tpt::StepState* out);
   int prefill(const uint32_t* ids, int n, int pos0, uint32_t* next_out, float* logits_out);
+  int prefill_steps(int n, int pos0);       // one decode step per position
+  int prefill_batched(int n, int pos0);     // GEMM path; ids already in ids_host
+  int prefill_scratch(int T, int n_chunks);
   // fn(user, s, tok) receives the token step s produced, in order; non-zero stops the run.
   typedef int (*StepFn)(void* user, int s, uint32_t tok);
   int decode_stream(uint32_t first, int pos0, int n_steps, StepFn fn, void* user, int* n_delivered);

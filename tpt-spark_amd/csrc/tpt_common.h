@@ -108,6 +108,40 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   v = sum16(v);
   return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
 }
+// candle BlockQ8K::from_float for one 256-element block held by a wave, 4 values per lane
+// (lane l holds elements 4l .. 4l+3): the signed value of largest |x| (first occurrence wins
+// ties), iscale = -128/max, q = round-half-away(iscale * x) clamped to [-128, 127], d = 1/iscale,
+// per-16 sums.  Returns the packed 4 int8 of the lane; *qsum16 = the sum of its 16-group (valid
+// on every lane of the group of 4), *d = the block scale (all lanes).
+__device__ __forceinline__ int q8k_block_wave(const float e[4], int* qsum16, float* d) {
+  const float la = fmaxf(fmaxf(fabsf(e[0]), fabsf(e[1])), fmaxf(fabsf(e[2]), fabsf(e[3])));
+  const float amax = wave_max_dpp(la);
+  const float mine = fabsf(e[0]) == amax ? e[0] : fabsf(e[1]) == amax ? e[1]
+                     : fabsf(e[2]) == amax ? e[2] : e[3];
+  const unsigned long long hit = __ballot(la == amax);
+  const int first = hit ? (int)__builtin_ctzll(hit) : 0;
+  const float mx = readlane_f(mine, first);
+  int packed = 0, qsum = 0;
+  float dd = 0.f;
+  if (amax != 0.f) {
+    const float iscale = -128.f / mx;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      float r = roundf(iscale * e[j]);
+      r = fminf(r, 127.f);
+      r = fmaxf(r, -128.f);
+      const int q = (int)r;
+      qsum += q;
+      packed |= (q & 0xff) << (8 * j);
+    }
+    dd = 1.f / iscale;
+  }
+  qsum += __builtin_amdgcn_update_dpp(0, qsum, 0xB1, 0xF, 0xF, false);  // groups of 4 lanes
+  qsum += __builtin_amdgcn_update_dpp(0, qsum, 0x4E, 0xF, 0xF, false);
+  *qsum16 = qsum;
+  *d = dd;
+  return packed;
+}
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));

@@ -18,7 +18,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K = 0, 1, 8, 12, 14
 BLOCK = {TYPE_F32: 1, TYPE_F16: 1, TYPE_Q8_0: 32, TYPE_Q4_K: 256, TYPE_Q6_K: 256}
 TYPE_SIZE = {TYPE_F32: 4, TYPE_F16: 2, TYPE_Q8_0: 34, TYPE_Q4_K: 144, TYPE_Q6_K: 210}
-ACT_Q8, ACT_F32 = 0, 1
+ACT_Q8, ACT_F32, ACT_F16 = 0, 1, 2
 
 ERR_INVALID, ERR_HIP, ERR_IO, ERR_FORMAT, ERR_UNSUPPORTED, ERR_CANCELLED, ERR_STATE, ERR_OOM = \
     -1, -2, -3, -4, -5, -6, -7, -8
@@ -98,6 +98,8 @@ EXPORTS = {
     "tpt_bench_gemv": ([P, I32, P, I32, P, P, I32, I32, I32, P], I32),
     "tpt_bench_attn": ([P, P, P, P, I32, P, I32, I32, I32, I32, I32, I32, I32, P], I32),
     "tpt_bench_copy": ([P, P, P, SZ, I32, P], I32),
+    "tpt_gemm": ([P, I32, P, P, P, I32, I32, I32, I32], I32),
+    "tpt_bench_gemm": ([P, I32, P, P, P, I32, I32, I32, I32, I32, P], I32),
 }
 
 
@@ -254,6 +256,19 @@ class Context:
         arr = (C.c_void_p * len(wbufs))(*[w.ptr for w in wbufs])
         ms = C.c_float()
         check(lib().tpt_bench_gemv(self.h, qtype, arr, len(wbufs), xbuf.ptr, ybuf.ptr, K, N, iters,
+                                   C.byref(ms)))
+        return ms.value
+
+    def gemm(self, qtype, wbuf, xbuf, M, K, N, act=ACT_Q8):
+        """Prefill GEMM Y[M,N] = X[M,K] . W[N,K]^T (X fp32 rows on the device)."""
+        y = self.alloc(M * N * 4)
+        check(lib().tpt_gemm(self.h, qtype, wbuf.ptr, xbuf.ptr, y.ptr, M, K, N, act))
+        return y.download(np.float32, M * N).reshape(M, N)
+
+    def bench_gemm(self, qtype, wbuf, xbuf, ybuf, M, K, N, iters, act=ACT_Q8):
+        """Sum of dispatch-stamped event intervals over iters GEMM launches; returns ms."""
+        ms = C.c_float()
+        check(lib().tpt_bench_gemm(self.h, qtype, wbuf.ptr, xbuf.ptr, ybuf.ptr, M, K, N, act, iters,
                                    C.byref(ms)))
         return ms.value
 
