@@ -97,6 +97,11 @@ int tpt_gemv_rmsnorm(tpt_ctx* ctx, int type, const void* w, const float* x,
 /* y = rmsnorm(x) with weight w.  Replaces rms_norm.wgsl:22-65 (n_rows = 1). */
 int tpt_rmsnorm(tpt_ctx* ctx, const float* x, const float* w, float* y, int n, float eps);
 
+/* y[i] = silu(g[i]) * up[i] with silu(t) = t / (1 + exp(-t)) in f32 (candle's silu; the decode
+ * and prefill paths fuse the same device function into their GEMV / activation kernels).
+ * Replaces silu.wgsl:20-29 (in place there; y may alias g here). */
+int tpt_swiglu(tpt_ctx* ctx, const float* g, const float* up, float* y, int n);
+
 /* In-place interleaved RoPE of n_heads heads of hd at position pos, using host-built f32
  * tables cos_t/sin_t [>= pos+1][hd/2] in device memory.  Replaces rope.wgsl:23-51
  * (dispatch_rope, wgpu_engine.rs:625-640) with candle's rope_i pairing. */
@@ -181,6 +186,17 @@ int tpt_model_decode_greedy(tpt_model* m, uint32_t first, int pos0, int n_steps,
                             int64_t stop_token, uint32_t* tokens_out);
 /* Copy the current residual stream (fp32 [embed]) to host memory (parity tests). */
 int tpt_model_hidden(tpt_model* m, float* out_host);
+/* Layer-range forward for parity checks (no counterpart in the reference): runs decoder layers
+ * [l0, l1) on n caller-given residual rows x_in (host fp32 [n][embed]) at positions
+ * pos0 .. pos0+n-1 and writes the resulting rows to x_out (host, same shape).  The layers' K/V
+ * rows at those positions are written as a forward pass writes them.  path 0: the batched
+ * prefill kernels (MFMA GEMMs; needs every layer matrix Q4_K, else TPT_ERR_UNSUPPORTED);
+ * path 1: the decode-step kernels, one position after another. */
+int tpt_model_run_layers(tpt_model* m, const float* x_in, int n, int pos0, int l0, int l1, int path,
+                         float* x_out);
+/* Copy one layer's K and V cache (each [n_kv_heads][max_ctx][head_dim] of the model's kv_type)
+ * to host memory, for cache-layout parity checks (no counterpart in the reference). */
+int tpt_model_kv_read(tpt_model* m, int layer, void* k_host, void* v_host);
 
 /* ------------------------------------------------------------------ engine (LlmEngine) */
 /* Mirrors `trait LlmEngine` (src-tauri/src/engine/mod.rs:62-82) for an engine-hip backend.

@@ -235,6 +235,14 @@ int orc_quantize_q8_0(const float* x, int64_t k, orc_blk_q8_0* y) {
 
 /* ------------------------------------------------------------------ vec_dot */
 
+/* Summation-order variant (test instrument, off by default): when set, each super-block's
+ * integer lanes are added first and one f32 term per block (d * sum - dmin * mins) joins a single
+ * running sum -- the order of a SIMD kernel that reduces lanes inside the block, instead of the
+ * generic path's eight f32 lane accumulators.  Same integers, different f32 rounding. */
+static int g_dot_block_order = 0;
+
+void orc_set_dot_block_order(int on) { g_dot_block_order = on != 0; }
+
 /* candle BlockQ4K::vec_dot_unopt (ggml generic ggml_vec_dot_q4_K_q8_K): 8 integer lanes
  * per block, f32 lane sums across blocks, mins subtracted through bsums. */
 static float vec_dot_q4k_q8k(int64_t n, const orc_blk_q4k* x, const orc_blk_q8k* y) {
@@ -270,8 +278,14 @@ static float vec_dot_q4k_q8k(int64_t n, const orc_blk_q4k* x, const orc_blk_q8k*
       }
     }
     const float d = orc_fp16_to_f32(x[i].d) * y[i].d;
-    for (int l = 0; l < 8; l++) sums[l] += d * (float)aux32[l];
     const float dmin = orc_fp16_to_f32(x[i].dmin) * y[i].d;
+    if (g_dot_block_order) {
+      int32_t t = 0;
+      for (int l = 0; l < 8; l++) t += aux32[l];
+      sumf += d * (float)t - dmin * (float)sumi;
+      continue;
+    }
+    for (int l = 0; l < 8; l++) sums[l] += d * (float)aux32[l];
     sumf -= dmin * (float)sumi;
   }
   float s = 0.f;
@@ -312,6 +326,12 @@ static float vec_dot_q6k_q8k(int64_t n, const orc_blk_q6k* x, const orc_blk_q8k*
       for (int l = 0; l < 8; l++) aux32[l] += scale * (float)aux16[l];
     }
     const float d = orc_fp16_to_f32(x[i].d) * y[i].d;
+    if (g_dot_block_order) {
+      float t = 0.f;
+      for (int l = 0; l < 8; l++) t += aux32[l];
+      sums[0] += t * d;
+      continue;
+    }
     for (int l = 0; l < 8; l++) sums[l] += aux32[l] * d;
   }
   float s = 0.f;
@@ -450,8 +470,8 @@ void orc_rope_i(float* x, int n_heads, int hd, const float* c, const float* s) {
 
 /* quantized_llama LayerWeights::forward_attn, non-metal branch: repeat_kv (head h reads kv
  * head h / (nq/nkv)), scores = (q.k) * f32(1/sqrt(hd)), softmax_last_dim, p.v */
-void orc_attention(const float* q, const float* kc, const float* vc, int nq, int nkv, int hd,
-                   int L, int L_stride, float* o) {
+static void attention_impl(const float* q, const float* kc, const float* vc, int nq, int nkv, int hd,
+                           int L, int L_stride, float* o, int fma) {
   const float scale = (float)(1.0 / sqrt((double)hd));
   float* sc = (float*)malloc(sizeof(float) * (size_t)L);
   const int rep = nq / nkv;
@@ -463,7 +483,7 @@ void orc_attention(const float* q, const float* kc, const float* vc, int nq, int
     float mx = -INFINITY;
     for (int p = 0; p < L; p++) {
       float s = 0.f;
-      for (int d = 0; d < hd; d++) s += qh[d] * K[(size_t)p * hd + d];
+      for (int d = 0; d < hd; d++) s = fma ? fmaf(qh[d], K[(size_t)p * hd + d], s) : s + qh[d] * K[(size_t)p * hd + d];
       s = s * scale;
       sc[p] = s;
       if (s > mx) mx = s;
@@ -477,11 +497,16 @@ void orc_attention(const float* q, const float* kc, const float* vc, int nq, int
     float* oh = o + (size_t)h * hd;
     for (int d = 0; d < hd; d++) {
       float acc = 0.f;
-      for (int p = 0; p < L; p++) acc += sc[p] * V[(size_t)p * hd + d];
+      for (int p = 0; p < L; p++) acc = fma ? fmaf(sc[p], V[(size_t)p * hd + d], acc) : acc + sc[p] * V[(size_t)p * hd + d];
       oh[d] = acc;
     }
   }
   free(sc);
+}
+
+void orc_attention(const float* q, const float* kc, const float* vc, int nq, int nkv, int hd,
+                   int L, int L_stride, float* o) {
+  attention_impl(q, kc, vc, nq, nkv, hd, L, L_stride, o, 0);
 }
 
 /* f32::total_cmp key */
@@ -550,6 +575,7 @@ struct orc_model {
   orc_layer* layers;
   /* runtime state */
   int max_pos, kv_f16;
+  int attn_fma; /* attention dots as fused multiply-adds (candle's gemm crate on an FMA host) */
   float *kcache, *vcache; /* [layer][kvh][max_pos][hd] */
   float* hidden;          /* last position's residual stream */
 };
@@ -757,6 +783,11 @@ const void* orc_model_tensor(const orc_model* m, const char* name, int* type, in
   return t->data;
 }
 
+int orc_model_set_attn_fma(orc_model* m, int on) {
+  m->attn_fma = on != 0;
+  return 0;
+}
+
 int orc_model_reset(orc_model* m, int max_pos, int kv_f16) {
   const orc_model_cfg* c = &m->cfg;
   free(m->kcache);
@@ -778,13 +809,14 @@ static int mm(const orc_tensor* w, int64_t rows, const float* x, float* y, int n
   return orc_matmul(w->type, rows, w->ne[0], w->ne[1], x, w->data, y, nt);
 }
 
-/* quantized_llama::ModelWeights::forward restated for tokens at pos0..pos0+n-1 */
-int orc_model_forward(orc_model* m, const uint32_t* tok, int n, int pos0, float* logits, int nt) {
+/* Decoder layers [l0, l1) of quantized_llama::ModelWeights::forward on the residual rows X
+ * ([n][embed], updated in place) at positions pos0..pos0+n-1, writing the layers' K/V rows;
+ * trace, when given, receives the rows entering each layer of the range and leaving the last
+ * ([l1 - l0 + 1][n][embed]). */
+static int layers_forward(orc_model* m, float* X, int n, int pos0, int l0, int l1, int nt, float* trace) {
   const orc_model_cfg* c = &m->cfg;
-  if (!m->kcache || pos0 + n > m->max_pos || n <= 0) return -1;
   const int H = c->embed, hd = c->head_dim, nq = c->n_heads, nkv = c->n_kv_heads, F = c->ffn;
   const int qd = nq * hd, kd = nkv * hd, half = c->rope_dim / 2;
-  float* X = (float*)malloc(sizeof(float) * (size_t)n * H);
   float* XN = (float*)malloc(sizeof(float) * (size_t)n * H);
   float* Q = (float*)malloc(sizeof(float) * (size_t)n * qd);
   float* K = (float*)malloc(sizeof(float) * (size_t)n * kd);
@@ -797,14 +829,9 @@ int orc_model_forward(orc_model* m, const uint32_t* tok, int n, int pos0, float*
   float* sn = (float*)malloc(sizeof(float) * (size_t)(pos0 + n) * half);
   int rc = 0;
   rope_rows(c->rope_dim, c->rope_base, pos0, pos0 + n, cs, sn);
-  /* embedding: candle dequantizes token_embd to f32 and index_selects rows */
-  for (int t = 0; t < n; t++) {
-    if (tok[t] >= (uint32_t)c->vocab) { rc = -2; goto done; }
-    orc_dequant(m->tok_embd->type, m->tok_embd->data + (size_t)tok[t] * row_bytes(m->tok_embd),
-                X + (size_t)t * H, H);
-  }
-  for (int l = 0; l < c->n_layers; l++) {
+  for (int l = l0; l < l1; l++) {
     const orc_layer* L = &m->layers[l];
+    if (trace) memcpy(trace + (size_t)(l - l0) * n * H, X, sizeof(float) * (size_t)n * H);
     for (int t = 0; t < n; t++) orc_rmsnorm(X + (size_t)t * H, L->attn_norm, H, c->eps, XN + (size_t)t * H);
     if ((rc = mm(L->q, n, XN, Q, nt)) || (rc = mm(L->k, n, XN, K, nt)) || (rc = mm(L->v, n, XN, V, nt))) goto done;
     const size_t lstride = (size_t)nkv * m->max_pos * hd;
@@ -824,7 +851,8 @@ int orc_model_forward(orc_model* m, const uint32_t* tok, int n, int pos0, float*
     }
     /* causal: position p attends to 0..p (the masked_fill(-inf) rows are exp()=0) */
     for (int t = 0; t < n; t++)
-      orc_attention(Q + (size_t)t * qd, kc, vc, nq, nkv, hd, pos0 + t + 1, m->max_pos, A + (size_t)t * qd);
+      attention_impl(Q + (size_t)t * qd, kc, vc, nq, nkv, hd, pos0 + t + 1, m->max_pos, A + (size_t)t * qd,
+                     m->attn_fma);
     if ((rc = mm(L->o, n, A, O, nt))) goto done;
     for (size_t i = 0; i < (size_t)n * H; i++) X[i] = O[i] + X[i];
     for (int t = 0; t < n; t++) orc_rmsnorm(X + (size_t)t * H, L->ffn_norm, H, c->eps, XN + (size_t)t * H);
@@ -833,12 +861,57 @@ int orc_model_forward(orc_model* m, const uint32_t* tok, int n, int pos0, float*
     if ((rc = mm(L->down, n, G, O, nt))) goto done;
     for (size_t i = 0; i < (size_t)n * H; i++) X[i] = O[i] + X[i];
   }
+  if (trace) memcpy(trace + (size_t)(l1 - l0) * n * H, X, sizeof(float) * (size_t)n * H);
+done:
+  free(XN); free(Q); free(K); free(V); free(A); free(O); free(G); free(U); free(cs); free(sn);
+  return rc;
+}
+
+/* quantized_llama::ModelWeights::forward restated for tokens at pos0..pos0+n-1; trace, when
+ * given, receives the residual rows entering each layer and leaving the last
+ * ([n_layers + 1][n][embed]) */
+int orc_model_forward_trace(orc_model* m, const uint32_t* tok, int n, int pos0, float* logits, int nt,
+                            float* trace) {
+  const orc_model_cfg* c = &m->cfg;
+  if (!m->kcache || pos0 + n > m->max_pos || n <= 0) return -1;
+  const int H = c->embed;
+  float* X = (float*)malloc(sizeof(float) * (size_t)n * H);
+  float* XN = (float*)malloc(sizeof(float) * (size_t)H);
+  int rc = 0;
+  /* embedding: candle dequantizes token_embd to f32 and index_selects rows */
+  for (int t = 0; t < n; t++) {
+    if (tok[t] >= (uint32_t)c->vocab) { rc = -2; goto done; }
+    orc_dequant(m->tok_embd->type, m->tok_embd->data + (size_t)tok[t] * row_bytes(m->tok_embd),
+                X + (size_t)t * H, H);
+  }
+  if ((rc = layers_forward(m, X, n, pos0, 0, c->n_layers, nt, trace))) goto done;
   memcpy(m->hidden, X + (size_t)(n - 1) * H, sizeof(float) * H);
   orc_rmsnorm(X + (size_t)(n - 1) * H, m->output_norm, H, c->eps, XN);
   rc = mm(m->output, 1, XN, logits, nt);
 done:
-  free(X); free(XN); free(Q); free(K); free(V); free(A); free(O); free(G); free(U); free(cs); free(sn);
+  free(X); free(XN);
   return rc;
+}
+
+int orc_model_run_layers(orc_model* m, const float* x_in, int n, int pos0, int l0, int l1, float* x_out,
+                         int nt) {
+  const orc_model_cfg* c = &m->cfg;
+  if (!m->kcache || pos0 + n > m->max_pos || n <= 0 || l0 < 0 || l1 > c->n_layers || l0 > l1) return -1;
+  memcpy(x_out, x_in, sizeof(float) * (size_t)n * c->embed);
+  return layers_forward(m, x_out, n, pos0, l0, l1, nt, NULL);
+}
+
+int orc_model_forward(orc_model* m, const uint32_t* tok, int n, int pos0, float* logits, int nt) {
+  return orc_model_forward_trace(m, tok, n, pos0, logits, nt, NULL);
+}
+
+int orc_model_kv(const orc_model* m, int layer, float* k_out, float* v_out) {
+  const orc_model_cfg* c = &m->cfg;
+  if (!m->kcache || layer < 0 || layer >= c->n_layers) return -1;
+  const size_t n = (size_t)c->n_kv_heads * m->max_pos * c->head_dim;
+  memcpy(k_out, m->kcache + (size_t)layer * n, n * sizeof(float));
+  memcpy(v_out, m->vcache + (size_t)layer * n, n * sizeof(float));
+  return 0;
 }
 
 int orc_model_last_hidden(const orc_model* m, float* out) {

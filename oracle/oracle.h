@@ -94,12 +94,33 @@ orc_model* orc_model_open(const char* gguf_path, char* err, int errlen);
 void orc_model_close(orc_model* m);
 void orc_model_get_cfg(const orc_model* m, orc_model_cfg* cfg);
 /* kv_f16: 1 rounds cached K/V to fp16 (mirrors the GPU cache), 0 keeps f32 like candle */
+/* The attention dot products as fused multiply-adds (on) or separate multiply and add (off, the
+ * default).  candle computes q.k^T and att.v with the gemm crate, which picks FMA kernels at
+ * run time on hosts that have FMA (gemm-0.17 x86 dispatch), so both are candle's results on
+ * some CPU; the spread between them bounds how closely any other summation order can be
+ * expected to track candle on an ill-conditioned model. */
+int orc_model_set_attn_fma(orc_model* m, int on);
 int orc_model_reset(orc_model* m, int max_pos, int kv_f16);
 /* Batched forward of n tokens at positions pos0..pos0+n-1 (causal); writes last-position
  * logits [vocab].  Mirrors ModelWeights::forward(&[1,n], pos0). nthreads as orc_matmul. */
 int orc_model_forward(orc_model* m, const uint32_t* tokens, int n, int pos0, float* logits,
                       int nthreads);
 /* read back hidden state after the last forward (final residual stream, pre-norm) */
+/* forward that also records the residual rows entering each layer and leaving the last into
+ * trace ([n_layers + 1][n][embed] floats) */
+int orc_model_forward_trace(orc_model* m, const uint32_t* tokens, int n, int pos0, float* logits,
+                            int nthreads, float* trace);
+/* Decoder layers [l0, l1) on caller-given residual rows x_in ([n][embed]) at positions
+ * pos0..pos0+n-1 (writing those layers' K/V rows); result rows to x_out. */
+int orc_model_run_layers(orc_model* m, const float* x_in, int n, int pos0, int l0, int l1, float* x_out,
+                         int nthreads);
+/* Summation-order variant of the k-quant dot products (off: candle's generic vec_dot order;
+ * on: integer lanes reduced inside each super-block, one f32 term per block).  A test
+ * instrument: the same integers with another f32 rounding, to measure how far a model's
+ * outputs move under a change of summation order alone. */
+void orc_set_dot_block_order(int on);
+/* copy of one layer's K and V cache, each [n_kv_heads][max_pos][head_dim] f32 */
+int orc_model_kv(const orc_model* m, int layer, float* k_out, float* v_out);
 int orc_model_last_hidden(const orc_model* m, float* out);
 
 /* raw tensor lookup for tests: returns pointer into the mmapped file or NULL */

@@ -53,6 +53,11 @@ def lib():
         L.orc_model_reset.argtypes = [P, I32, I32]
         L.orc_model_forward.argtypes = [P, P, I32, I32, P, I32]
         L.orc_model_last_hidden.argtypes = [P, P]
+        L.orc_model_forward_trace.argtypes = [P, P, I32, I32, P, I32, P]
+        L.orc_model_set_attn_fma.argtypes = [P, I32]
+        L.orc_model_kv.argtypes = [P, I32, P, P]
+        L.orc_model_run_layers.argtypes = [P, P, I32, I32, I32, I32, P, I32]
+        L.orc_set_dot_block_order.argtypes = [I32]
         L.orc_model_tensor.argtypes = [P, C.c_char_p, P, P, P]
         L.orc_model_tensor.restype = P
         _LIB = L
@@ -149,6 +154,11 @@ def attention(q, kc, vc, nq, nkv, hd, L):
     return o
 
 
+def set_dot_block_order(on):
+    """k-quant dot products in the block-reduced f32 order (a test instrument; off = candle's)."""
+    lib().orc_set_dot_block_order(int(on))
+
+
 def argmax(logits):
     logits = np.ascontiguousarray(logits, np.float32)
     return int(lib().orc_argmax(_p(logits), logits.size))
@@ -187,8 +197,13 @@ class Model:
         lib().orc_model_get_cfg(self.h, C.byref(c))
         self.cfg = {n: getattr(c, n) for n, _ in _Cfg._fields_}
 
+    def set_attn_fma(self, on):
+        """Attention dots as fused multiply-adds (the gemm crate's kernels on an FMA host)."""
+        lib().orc_model_set_attn_fma(self.h, int(on))
+
     def reset(self, max_pos, kv_f16=False):
         assert lib().orc_model_reset(self.h, max_pos, int(kv_f16)) == 0
+        self.max_pos = max_pos
 
     def forward(self, tokens, pos0, nthreads=0):
         toks = np.ascontiguousarray(tokens, np.uint32)
@@ -197,6 +212,35 @@ class Model:
         if rc:
             raise RuntimeError(f"orc_model_forward rc={rc}")
         return logits
+
+    def forward_trace(self, tokens, pos0, nthreads=0):
+        """forward() that also returns the residual rows entering each layer and leaving the
+        last: trace[l] is layer l's input [n, embed], trace[n_layers] the final rows."""
+        toks = np.ascontiguousarray(tokens, np.uint32)
+        logits = np.empty(self.cfg["vocab"], np.float32)
+        trace = np.empty((self.cfg["n_layers"] + 1, toks.size, self.cfg["embed"]), np.float32)
+        rc = lib().orc_model_forward_trace(self.h, _p(toks), toks.size, pos0, _p(logits), nthreads,
+                                           _p(trace))
+        if rc:
+            raise RuntimeError(f"orc_model_forward_trace rc={rc}")
+        return logits, trace
+
+    def run_layers(self, x, pos0, l0, l1, nthreads=0):
+        """Decoder layers [l0, l1) on residual rows x [n, embed] at positions pos0 ..."""
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, self.cfg["embed"])
+        out = np.empty_like(x)
+        rc = lib().orc_model_run_layers(self.h, _p(x), x.shape[0], pos0, l0, l1, _p(out), nthreads)
+        if rc:
+            raise RuntimeError(f"orc_model_run_layers rc={rc}")
+        return out
+
+    def kv(self, layer):
+        """Layer's K and V caches [n_kv_heads, max_pos, head_dim] (f32; fp16-rounded values in
+        the fp16 mode)."""
+        shape = (self.cfg["n_kv_heads"], self.max_pos, self.cfg["head_dim"])
+        k, v = np.empty(shape, np.float32), np.empty(shape, np.float32)
+        assert lib().orc_model_kv(self.h, layer, _p(k), _p(v)) == 0
+        return k, v
 
     def last_hidden(self):
         out = np.empty(self.cfg["embed"], np.float32)

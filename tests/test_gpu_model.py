@@ -249,3 +249,224 @@ def test_load_errors(ctx, tiny_gguf, tmp_path):
     with pytest.raises(tpthip.TptError) as e:
         tpthip.Model(ctx, bad)
     assert e.value.code == tpthip.ERR_FORMAT
+
+
+# ---------------------------------------------------------------- batched prefill
+
+# fp16 K/V rounding can flip under f32 summation-order differences, and a flipped K/V entry
+# feeds every later position: over a 150-token prompt the oracle itself moves by 0.011 (block-
+# reduced dot products) to 0.013 (fused-multiply-add attention) in max-abs logits with the fp16
+# cache, and by 2e-7 with the f32 cache.
+LONG_TOL = {"f32": 1e-3, "f16": 4e-2}
+
+
+def test_batched_prefill_equals_steps(ctx, tiny_gguf, kv):
+    """The MFMA prefill and the one-decode-step-per-position prefill compute the same Q8_K
+    integer products; only f32 summation order differs."""
+    prompt = [int(t) for t in np.random.default_rng(5).integers(0, 1024, 150)]
+    m_b = tpthip.Model(ctx, tiny_gguf, max_ctx=256, kv_type=KV_TYPE[kv])
+    os.environ["TPT_HIP_PREFILL"] = "steps"
+    try:
+        m_s = tpthip.Model(ctx, tiny_gguf, max_ctx=256, kv_type=KV_TYPE[kv])
+    finally:
+        del os.environ["TPT_HIP_PREFILL"]
+    try:
+        nb, lb = m_b.prefill(prompt, 0, logits=True)
+        ns, ls = m_s.prefill(prompt, 0, logits=True)
+        print("batched vs steps max-abs", np.abs(lb - ls).max())
+        assert nb == ns
+        assert np.abs(lb - ls).max() < LONG_TOL[kv]
+        if kv == "f32":  # the caches agree: the next greedy tokens match
+            assert m_b.decode_greedy(nb, len(prompt), 12) == m_s.decode_greedy(ns, len(prompt), 12)
+    finally:
+        m_b.close()
+        m_s.close()
+
+
+def test_tiny_long_prompt_matches_oracle(ctx, tiny_gguf, tiny_oracle, kv):
+    """150-token prompt (several attention chunks on the step path) on both prefill paths."""
+    prompt = [int(t) for t in np.random.default_rng(5).integers(0, 1024, 150)]
+    tiny_oracle.reset(256, kv_f16=(kv == "f16"))
+    ref = tiny_oracle.forward(prompt, 0)
+    for path in ("batched", "steps"):
+        if path == "steps":
+            os.environ["TPT_HIP_PREFILL"] = "steps"
+        try:
+            m = tpthip.Model(ctx, tiny_gguf, max_ctx=256, kv_type=KV_TYPE[kv])
+        finally:
+            os.environ.pop("TPT_HIP_PREFILL", None)
+        try:
+            nxt, lg = m.prefill(prompt, 0, logits=True)
+        finally:
+            m.close()
+        print(path, "max-abs vs oracle", np.abs(lg - ref).max())
+        assert np.abs(lg - ref).max() < LONG_TOL[kv], path
+        assert nxt == oracle.argmax(ref)
+
+
+@pytest.fixture(scope="module")
+def gguf_1b(tmp_path_factory):
+    """Llama 1B shape (16 layers, hidden 2048, 32/8 heads, head_dim 64, FFN 8192, vocab 128256,
+    theta 500000), Q4_K_M, weights N(0, 0.02), norms 1."""
+    path = str(tmp_path_factory.mktemp("m1b") / "llama-1b-shape-q4_k_m.gguf")
+    synth.write_llama(path, synth.LLAMA_1B, seed=1234, nthreads=min(os.cpu_count() or 1, 16))
+    yield path
+    os.remove(path)
+
+
+PROMPT_1B = [int(t) for t in np.random.default_rng(128).integers(0, 128256, 128)]
+_TRACES = {}
+
+
+def oracle_trace_1b(path, kv_mode):
+    """The oracle's residual stream at every layer boundary for the 128-token prompt (batched
+    forward), then for one greedy decode token at position 128; cached per cache mode."""
+    if kv_mode not in _TRACES:
+        om = oracle.Model(path)
+        om.reset(256, kv_f16=(kv_mode == "f16"))
+        nt = min(os.cpu_count() or 1, 16)
+        logits, tr = om.forward_trace(PROMPT_1B, 0, nt)
+        tok = oracle.argmax(logits)
+        _, tr2 = om.forward_trace([tok], len(PROMPT_1B), nt)
+        kvs = [om.kv(l) for l in range(tr.shape[0] - 1)] if kv_mode == "f32" else None
+        om.close()
+        _TRACES[kv_mode] = (logits, tr, tok, tr2, kvs)
+    return _TRACES[kv_mode]
+
+
+def _rel_l2(a, b):
+    return float(np.linalg.norm((a - b).ravel()) / np.linalg.norm(b.ravel()))
+
+
+def _row_rel(a, b):
+    return np.linalg.norm(a - b, axis=-1) / np.linalg.norm(b, axis=-1)
+
+
+@pytest.mark.timeout(900)
+def test_1b_ops_on_oracle_layer_inputs(ctx, gguf_1b):
+    """Every operation of a decoder layer at the 1B shape, fed the oracle's own intermediate
+    values of layers 0, 5 and 15 (128 positions), against the oracle on the same values:
+    RMSNorm, the Q4_K GEMV (Q8_K activations quantized on the GPU) and the MFMA GEMM for
+    Q, Wo, gate and down, RoPE, attention over the oracle's cache, SwiGLU.  Identical inputs
+    leave only f32 rounding: per-row relative error <= 2e-6 (attention 1e-5); SiLU equal but
+    for < 0.1% of elements, which differ by at most two ulp (the host libm's expf is not
+    correctly rounded for every argument; the device rounds the f64 exponential once, and a
+    last-place change of exp(-g) passes through 1 + e and the divide)."""
+    _, tr, _, _, kvs = oracle_trace_1b(gguf_1b, "f32")
+    om = oracle.Model(gguf_1b)
+    H, hd, nq, nkv, F, eps, n = 2048, 64, 32, 8, 8192, 1e-5, len(PROMPT_1B)
+    cos_t, sin_t = oracle.rope_tables(hd, 500000.0, 256)
+    dcos, dsin = ctx.to_device(cos_t), ctx.to_device(sin_t)
+    worst = {}
+
+    def check(name, got, want, tol=2e-6):
+        e = float(_row_rel(got, want).max())
+        worst[name] = max(worst.get(name, 0.0), e)
+        assert e <= tol, (name, e)
+
+    try:
+        for layer in (0, 5, 15):
+            X = tr[layer]
+            t = {k: om.tensor(f"blk.{layer}.{k}.weight") for k in
+                 ("attn_q", "attn_output", "ffn_gate", "ffn_down")}
+            an = om.tensor(f"blk.{layer}.attn_norm.weight")[3].view(np.float32)
+            fn = om.tensor(f"blk.{layer}.ffn_norm.weight")[3].view(np.float32)
+            dan, dfn = ctx.to_device(an), ctx.to_device(fn)
+            XN = np.stack([oracle.rmsnorm(x, an, eps) for x in X])
+            check("rmsnorm", np.stack([ctx.rmsnorm(ctx.to_device(x), dan, H, eps) for x in X]), XN)
+
+            def mat(key, A, N):
+                qt, _, _, raw = t[key]
+                want = oracle.matmul(qt, A, raw, N, 16)
+                dw = ctx.to_device(raw)
+                K = A.shape[1]
+                check(key + " gemv", np.stack([ctx.gemv(qt, dw, ctx.to_device(a), K, N) for a in A[:32]]),
+                      want[:32])
+                check(key + " gemm", ctx.gemm(qt, dw, ctx.to_device(A), A.shape[0], K, N), want)
+                return want
+
+            Q = mat("attn_q", XN, nq * hd)
+            Qr = np.stack([oracle.rope_i(Q[i], nq, hd, cos_t[i], sin_t[i]) for i in range(n)])
+            check("rope", np.stack([ctx.rope(ctx.to_device(Q[i].copy()), nq, hd, i, dcos, dsin)
+                                    for i in range(n)]), Qr)
+            kc, vc = kvs[layer]
+            dk, dv = ctx.to_device(kc), ctx.to_device(vc)
+            A = np.stack([oracle.attention(Qr[i], kc, vc, nq, nkv, hd, i + 1) for i in range(n)])
+            check("attention", np.stack([ctx.attn_decode(ctx.to_device(Qr[i]), dk, dv, nq, nkv, hd, i + 1,
+                                                         kc.shape[1], kv_type=tpthip.TYPE_F32)
+                                         for i in range(n)]), A, tol=1e-5)
+            Xm = mat("attn_output", A, H) + X
+            XN2 = np.stack([oracle.rmsnorm(x, fn, eps) for x in Xm])
+            G = mat("ffn_gate", XN2, F)
+            U = np.random.default_rng(layer).standard_normal(G.shape).astype(np.float32)
+            S = np.stack([np.array([oracle.silu(v) for v in G[i]], np.float32) for i in range(8)])
+            got = ctx.swiglu(ctx.to_device(G[:8]), ctx.to_device(np.ones_like(G[:8])), 8 * F).reshape(8, F)
+            ulps = float((np.abs(got - S) / np.spacing(np.abs(S))).max())
+            worst["silu ulp"] = max(worst.get("silu ulp", 0.0), ulps)
+            worst["silu differs"] = max(worst.get("silu differs", 0.0), float(np.mean(got != S)))
+            assert ulps <= 2 and np.mean(got != S) < 1e-3, ("silu", ulps, np.mean(got != S))
+            want = S * U[:8]
+            mat("ffn_down", want, H)
+    finally:
+        om.close()
+    print({k: f"{v:.1e}" for k, v in worst.items()})
+
+
+@pytest.mark.timeout(900)
+def test_1b_layers_teacher_forced(ctx, gguf_1b, kv):
+    """Each decoder layer at the 1B shape, fed the oracle's residual rows, against the oracle's
+    next rows: the 128 prompt positions through the batched MFMA kernels and through the
+    decode-step kernels, then position 128 on the decode path over the cache the batched run
+    left.  The ops agree to f32 rounding on identical inputs (the test above); here the Q8_K
+    activation quantization (and, in the fp16 mode, the fp16 K/V rounding) can flip under
+    those rounding differences, and a flip in one position's K/V input reaches every later
+    position through attention.  The oracle moves by the same amount under a change of its own
+    dot-product summation order (block-reduced instead of candle's eight f32 lanes), so the bar
+    is that size: relative L2 over the layer output <= 1e-2 (f32 cache) / 2e-2 (fp16 cache)."""
+    _, tr, _, tr2, _ = oracle_trace_1b(gguf_1b, kv)
+    tol = 1e-2 if kv == "f32" else 2e-2
+    n_layers = tr.shape[0] - 1
+    errs = {"batched": [], "steps": [], "decode": []}
+    mb = tpthip.Model(ctx, gguf_1b, max_ctx=256, kv_type=KV_TYPE[kv])
+    ms = tpthip.Model(ctx, gguf_1b, max_ctx=256, kv_type=KV_TYPE[kv])
+    try:
+        for l in range(n_layers):
+            errs["batched"].append(_rel_l2(mb.run_layers(tr[l], 0, l, l + 1, path=0), tr[l + 1]))
+            errs["steps"].append(_rel_l2(ms.run_layers(tr[l], 0, l, l + 1, path=1), tr[l + 1]))
+        for l in range(n_layers):
+            errs["decode"].append(_rel_l2(mb.run_layers(tr2[l], len(PROMPT_1B), l, l + 1, path=1),
+                                          tr2[l + 1]))
+    finally:
+        mb.close()
+        ms.close()
+    print({k: f"{max(v):.2e}" for k, v in errs.items()})
+    for k, v in errs.items():
+        assert max(v) < tol, (k, v)
+
+
+@pytest.mark.timeout(900)
+def test_1b_end_to_end_within_candle_spread(ctx, gguf_1b, kv):
+    """End to end at the 1B shape (128-token prompt, then greedy decode).  This random-init
+    model amplifies rounding: candle's own result moves by the same order when its attention
+    products switch between fused and separate multiply-adds (the gemm crate picks per host
+    CPU), and greedy sequences of the two diverge within a few tokens.  So the bar here is that
+    spread: the GPU's last-position logits stay within twice the oracle's FMA/non-FMA distance,
+    and the first greedy token (which the spread does not move) is identical."""
+    logits, _, tok, _, _ = oracle_trace_1b(gguf_1b, kv)
+    om = oracle.Model(gguf_1b)
+    om.set_attn_fma(True)
+    om.reset(256, kv_f16=(kv == "f16"))
+    alt = om.forward(PROMPT_1B, 0, min(os.cpu_count() or 1, 16))
+    om.close()
+    spread = float(np.abs(alt - logits).max())
+    m = tpthip.Model(ctx, gguf_1b, max_ctx=256, kv_type=KV_TYPE[kv])
+    try:
+        first, lg = m.prefill(PROMPT_1B, 0, logits=True)
+        dev = float(np.abs(lg - logits).max())
+        print(f"gpu-oracle {dev:.3f}, oracle fma-nonfma spread {spread:.3f}")
+        assert first == tok == oracle.argmax(alt)
+        assert dev < 2 * spread + 1e-2
+        toks = m.decode_greedy(first, len(PROMPT_1B), 31)
+        assert len(toks) == 31 and all(0 <= t < 128256 for t in toks)
+    finally:
+        m.close()

@@ -170,6 +170,12 @@ int tpt_rmsnorm(tpt_ctx* c, const float* x, const float* w, float* y, int n, flo
   return launch_rmsnorm(x, w, y, n, eps, c->stream);
 }
 
+int tpt_swiglu(tpt_ctx* c, const float* g, const float* u, float* y, int n) {
+  ENTER(c);
+  if (!g || !u || !y) return fail(TPT_ERR_INVALID, "swiglu: null pointer");
+  return launch_swiglu(g, u, y, n, c->stream);
+}
+
 int tpt_rope(tpt_ctx* c, float* x, int n_heads, int hd, int pos, const float* cos_t,
              const float* sin_t) {
   ENTER(c);

@@ -284,10 +284,10 @@ __global__ void __launch_bounds__(256) act_prep_kernel(const ActPrepArgs a) {
     float4 v = xr[i];
     if (ur) {
       const float4 u = ur[i];
-      v.x = v.x / (1.f + expf(-v.x)) * u.x;
-      v.y = v.y / (1.f + expf(-v.y)) * u.y;
-      v.z = v.z / (1.f + expf(-v.z)) * u.z;
-      v.w = v.w / (1.f + expf(-v.w)) * u.w;
+      v.x = silu_mul(v.x, u.x);
+      v.y = silu_mul(v.y, u.y);
+      v.z = silu_mul(v.z, u.z);
+      v.w = silu_mul(v.w, u.w);
     }
     return v;
   };

@@ -478,7 +478,7 @@ __global__ void __launch_bounds__(NT, 2) gemv_q8_kernel(const GemvArgs A, const 
     case EPI_SWIGLU:
       for (int i = tid; i < nrows; i += NT) {
         const float g = row_val(i, 0);
-        A.y[r0 + i] = g / (1.f + expf(-g)) * row_val(i, NMAT - 1);
+        A.y[r0 + i] = silu_mul(g, row_val(i, NMAT - 1));
       }
       break;
     case EPI_ARGMAX: {

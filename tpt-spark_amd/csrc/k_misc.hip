@@ -138,6 +138,13 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(const QkvPostArgs a) {
   }
 }
 
+// y[i] = silu(g[i]) * u[i] (the elementwise op the GEMV and GEMM epilogues fuse)
+__global__ void __launch_bounds__(256) swiglu_kernel(const float* g, const float* __restrict__ u,
+                                                     float* y, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = silu_mul(g[i], u[i]);
+}
+
 // candle_nn::ops::rms_norm: m = sqrt(sum(x^2)/n + eps); y = x / m * w (one workgroup)
 __global__ void __launch_bounds__(1024) rmsnorm_kernel(const float* __restrict__ x,
                                                        const float* __restrict__ w,
@@ -242,6 +249,13 @@ int launch_qkv_post(const QkvPostArgs& a, hipStream_t s) {
   if (a.pos0 < 0 || a.pos0 + a.T > a.max_ctx) return fail(TPT_ERR_INVALID, "qkv_post: positions past the cache");
   const int npair = (a.qd + 2 * a.kd) / 2;
   hipLaunchKernelGGL(qkv_post_kernel, dim3((unsigned)((npair + 255) / 256), (unsigned)a.T), dim3(256), 0, s, a);
+  TPT_HIP(hipGetLastError());
+  return TPT_OK;
+}
+
+int launch_swiglu(const float* g, const float* u, float* y, int n, hipStream_t s) {
+  if (n <= 0) return fail(TPT_ERR_INVALID, "swiglu: n must be positive");
+  hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, g, u, y, n);
   TPT_HIP(hipGetLastError());
   return TPT_OK;
 }

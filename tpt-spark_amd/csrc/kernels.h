@@ -94,6 +94,7 @@ int launch_act_prep(const ActPrepArgs& a, hipStream_t s);
 
 int launch_dequant(int type, const void* w, float* y, int64_t n, hipStream_t s);
 int launch_rmsnorm(const float* x, const float* w, float* y, int n, float eps, hipStream_t s);
+int launch_swiglu(const float* g, const float* u, float* y, int n, hipStream_t s);
 int launch_rope(float* x, int n_heads, int hd, int pos, const float* c, const float* sn,
                 hipStream_t s);
 int launch_copy(void* dst, const void* src, size_t bytes, hipStream_t s);

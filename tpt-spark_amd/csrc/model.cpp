@@ -312,12 +312,37 @@ int tpt_model::bucket_of(int L) const {
 int tpt_model::enqueue_step(int bucket, bool lm_head) {
   const int n_chunks = std::min(attn_default_chunks(bucket, desc.n_kv_heads), attn_max_chunks);
   const int chunk_len = attn_chunk_len(bucket, n_chunks);
+  int rc = launch_step_begin(st, prompt_dev, embd_type, embd, embd_row, desc.embed, desc.vocab, x,
+                             tok_log, stream);
+  if (rc) return rc;
+  for (int l = 0; l < desc.n_layers; l++)
+    if ((rc = enqueue_layer(l, n_chunks, chunk_len))) return rc;
+  if (lm_head) {
+    GemvArgs lh;
+    lh.w0 = out;
+    lh.row_stride = row_bytes(out_type, desc.embed);
+    lh.K = desc.embed;
+    lh.N = desc.vocab;
+    lh.x = x;
+    lh.norm_w = out_norm;
+    lh.eps = desc.rms_eps;
+    lh.prologue = PRO_RMSNORM;
+    lh.epilogue = EPI_ARGMAX;
+    lh.y = logits;
+    lh.amax = (unsigned long long*)((char*)st + offsetof(StepState, amax));  // device address
+    lh.state = st;
+    if ((rc = launch_gemv_q8(ctx, out_type, lh, stream))) return rc;
+  }
+  return TPT_OK;
+}
+
+// One decoder layer of a decode step on the residual stream x at position state->pos.
+int tpt_model::enqueue_layer(int l, int n_chunks, int chunk_len) {
   const int H = desc.embed, hd = desc.head_dim, nq = desc.n_heads, nkv = desc.n_kv_heads;
   const int qd = nq * hd, kd = nkv * hd, F = desc.ffn, mc = desc.max_ctx;
-  int rc = launch_step_begin(st, prompt_dev, embd_type, embd, embd_row, H, desc.vocab, x, tok_log, stream);
-  if (rc) return rc;
   const size_t layer_kv = (size_t)2 * nkv * mc * hd;
-  for (int l = 0; l < desc.n_layers; l++) {
+  int rc;
+  {
     const Layer& L = layers[l];
     uint8_t* kc = (uint8_t*)kv + (size_t)l * layer_kv * kv_elem;
     uint8_t* vc = kc + (size_t)nkv * mc * hd * kv_elem;
@@ -408,22 +433,6 @@ int tpt_model::enqueue_step(int bucket, bool lm_head) {
     dn.y = x;
     dn.resid = x;
     if ((rc = launch_gemv_q8(ctx, L.td, dn, stream))) return rc;
-  }
-  if (lm_head) {
-    GemvArgs lh;
-    lh.w0 = out;
-    lh.row_stride = row_bytes(out_type, H);
-    lh.K = H;
-    lh.N = desc.vocab;
-    lh.x = x;
-    lh.norm_w = out_norm;
-    lh.eps = desc.rms_eps;
-    lh.prologue = PRO_RMSNORM;
-    lh.epilogue = EPI_ARGMAX;
-    lh.y = logits;
-    lh.amax = (unsigned long long*)((char*)st + offsetof(StepState, amax));  // device address
-    lh.state = st;
-    if ((rc = launch_gemv_q8(ctx, out_type, lh, stream))) return rc;
   }
   return TPT_OK;
 }
@@ -516,69 +525,115 @@ int tpt_model::prefill_scratch(int T, int n_chunks) {
   return TPT_OK;
 }
 
+// Attention partition of a batched slice whose last position is Lmax - 1.
+static int slice_chunks(int Lmax) { return (Lmax + 511) / 512; }
+
 // Batched prefill of positions pos0 .. pos0+n-1 (ids in ids_host[pos0 ..]): slices of up to
 // kPrefillT positions run the whole layer stack as GEMMs (candle's batched forward,
-// candle_engine.rs:272-273: per layer rms_norm, Q/K/V, rope_i, KV append, causal attention,
-// Wo + residual, rms_norm, SwiGLU, down + residual), leaving the last position's residual
-// stream in x for the LM head.
+// candle_engine.rs:272-273), leaving the last position's residual stream in x for the LM head.
 int tpt_model::prefill_batched(int n, int pos0) {
-  const int H = desc.embed, hd = desc.head_dim, nq = desc.n_heads, nkv = desc.n_kv_heads;
-  const int qd = nq * hd, kd = nkv * hd, F = desc.ffn, mc = desc.max_ctx;
-  const size_t layer_kv = (size_t)2 * nkv * mc * hd;
   int rc;
   for (int c0 = 0; c0 < n; c0 += kPrefillT) {
     const int T = std::min(kPrefillT, n - c0), p0 = pos0 + c0;
-    const int Lmax = p0 + T;
-    int nch = (Lmax + 511) / 512;
-    const int cl = attn_chunk_len(Lmax, nch);
-    if ((rc = prefill_scratch(T, nch))) return rc;
+    if ((rc = prefill_scratch(T, slice_chunks(p0 + T)))) return rc;
     TPT_HIP(hipMemcpyAsync(pf_ids, ids_host + p0, (size_t)T * 4, hipMemcpyHostToDevice, stream));
-    if ((rc = launch_embed_rows(pf_ids, T, embd_type, embd, embd_row, H, pf_x, stream))) return rc;
-    auto prep = [&](const float* x, const float* x2, int K, const float* nw) {
-      ActPrepArgs a;
-      a.M = T; a.K = K; a.ldx = K; a.x = x; a.x2 = x2; a.norm_w = nw; a.eps = desc.rms_eps;
-      a.mode = GEMM_Q8K; a.aq = pf_aq; a.ad = pf_ad; a.as16 = pf_as16;
-      return launch_act_prep(a, stream);
-    };
-    auto gemm = [&](const uint8_t* w, int K, int N, float* y, int ldy, const float* resid) {
-      GemmArgs g;
-      g.M = T; g.N = N; g.K = K; g.mode = GEMM_Q8K;
-      g.w = w; g.w_stride = row_bytes(TPT_TYPE_Q4_K, K);
-      g.aq = pf_aq; g.ad = pf_ad; g.as16 = pf_as16;
-      g.y = y; g.ldy = ldy; g.resid = resid; g.ldr = ldy;
-      return launch_gemm_q4k(g, stream);
-    };
-    for (int l = 0; l < desc.n_layers; l++) {
-      const Layer& L = layers[l];
-      uint8_t* kc = (uint8_t*)kv + (size_t)l * layer_kv * kv_elem;
-      uint8_t* vc = kc + (size_t)nkv * mc * hd * kv_elem;
-      if ((rc = prep(pf_x, nullptr, H, L.attn_norm))) return rc;
-      const int ldq = qd + 2 * kd;
-      if (L.qkv_adjacent) {
-        if ((rc = gemm(L.q, H, ldq, pf_qkv, ldq, nullptr))) return rc;
-      } else {
-        if ((rc = gemm(L.q, H, qd, pf_qkv, ldq, nullptr)) || (rc = gemm(L.k, H, kd, pf_qkv + qd, ldq, nullptr)) ||
-            (rc = gemm(L.v, H, kd, pf_qkv + qd + kd, ldq, nullptr)))
-          return rc;
-      }
-      QkvPostArgs qp;
-      qp.qkv = pf_qkv; qp.T = T; qp.qd = qd; qp.kd = kd; qp.hd = hd; qp.q = pf_q;
-      qp.kcache = kc; qp.vcache = vc; qp.kv_type = desc.kv_type; qp.max_ctx = mc; qp.pos0 = p0;
-      qp.rope_cos = rope_cos; qp.rope_sin = rope_sin;
-      if ((rc = launch_qkv_post(qp, stream))) return rc;
-      AttnArgs at;
-      at.q = pf_q; at.ldq = qd; at.kc = kc; at.vc = vc; at.kv_type = desc.kv_type;
-      at.o = pf_att; at.ldo = qd; at.nq = nq; at.nkv = nkv; at.hd = hd; at.L_stride = mc;
-      at.L_host = p0 + 1; at.nqb = T; at.n_chunks = nch; at.chunk_len = cl; at.part = pf_part;
-      if ((rc = launch_attn_decode(at, stream))) return rc;
-      if ((rc = prep(pf_att, nullptr, qd, nullptr)) || (rc = gemm(L.o, qd, H, pf_x, H, pf_x))) return rc;
-      if ((rc = prep(pf_x, nullptr, H, L.ffn_norm)) || (rc = gemm(L.gate, H, F, pf_g, F, nullptr)) ||
-          (rc = gemm(L.up, H, F, pf_u, F, nullptr)))
-        return rc;
-      if ((rc = prep(pf_g, pf_u, F, nullptr)) || (rc = gemm(L.down, F, H, pf_x, H, pf_x))) return rc;
-    }
+    if ((rc = launch_embed_rows(pf_ids, T, embd_type, embd, embd_row, desc.embed, pf_x, stream))) return rc;
+    if ((rc = batched_layers(T, p0, 0, desc.n_layers))) return rc;
     // the last position's residual stream feeds the LM head
-    TPT_HIP(hipMemcpyAsync(x, pf_x + (size_t)(T - 1) * H, (size_t)H * 4, hipMemcpyDeviceToDevice, stream));
+    TPT_HIP(hipMemcpyAsync(x, pf_x + (size_t)(T - 1) * desc.embed, (size_t)desc.embed * 4,
+                           hipMemcpyDeviceToDevice, stream));
+  }
+  return TPT_OK;
+}
+
+// Layers [l0, l1) over the T residual rows in pf_x (positions p0 .. p0+T-1), per layer as
+// candle's forward orders it: rms_norm, Q/K/V, rope_i, KV append, causal attention, Wo +
+// residual, rms_norm, SwiGLU, down + residual.  The scratch must be sized for (T, p0 + T).
+int tpt_model::batched_layers(int T, int p0, int l0, int l1) {
+  const int H = desc.embed, hd = desc.head_dim, nq = desc.n_heads, nkv = desc.n_kv_heads;
+  const int qd = nq * hd, kd = nkv * hd, F = desc.ffn, mc = desc.max_ctx;
+  const size_t layer_kv = (size_t)2 * nkv * mc * hd;
+  const int Lmax = p0 + T, nch = slice_chunks(Lmax), cl = attn_chunk_len(Lmax, nch);
+  int rc;
+  auto prep = [&](const float* xx, const float* x2, int K, const float* nw) {
+    ActPrepArgs a;
+    a.M = T; a.K = K; a.ldx = K; a.x = xx; a.x2 = x2; a.norm_w = nw; a.eps = desc.rms_eps;
+    a.mode = GEMM_Q8K; a.aq = pf_aq; a.ad = pf_ad; a.as16 = pf_as16;
+    return launch_act_prep(a, stream);
+  };
+  auto gemm = [&](const uint8_t* w, int K, int N, float* y, int ldy, const float* resid) {
+    GemmArgs g;
+    g.M = T; g.N = N; g.K = K; g.mode = GEMM_Q8K;
+    g.w = w; g.w_stride = row_bytes(TPT_TYPE_Q4_K, K);
+    g.aq = pf_aq; g.ad = pf_ad; g.as16 = pf_as16;
+    g.y = y; g.ldy = ldy; g.resid = resid; g.ldr = ldy;
+    return launch_gemm_q4k(g, stream);
+  };
+  for (int l = l0; l < l1; l++) {
+    const Layer& L = layers[l];
+    uint8_t* kc = (uint8_t*)kv + (size_t)l * layer_kv * kv_elem;
+    uint8_t* vc = kc + (size_t)nkv * mc * hd * kv_elem;
+    if ((rc = prep(pf_x, nullptr, H, L.attn_norm))) return rc;
+    const int ldq = qd + 2 * kd;
+    if (L.qkv_adjacent) {
+      if ((rc = gemm(L.q, H, ldq, pf_qkv, ldq, nullptr))) return rc;
+    } else {
+      if ((rc = gemm(L.q, H, qd, pf_qkv, ldq, nullptr)) || (rc = gemm(L.k, H, kd, pf_qkv + qd, ldq, nullptr)) ||
+          (rc = gemm(L.v, H, kd, pf_qkv + qd + kd, ldq, nullptr)))
+        return rc;
+    }
+    QkvPostArgs qp;
+    qp.qkv = pf_qkv; qp.T = T; qp.qd = qd; qp.kd = kd; qp.hd = hd; qp.q = pf_q;
+    qp.kcache = kc; qp.vcache = vc; qp.kv_type = desc.kv_type; qp.max_ctx = mc; qp.pos0 = p0;
+    qp.rope_cos = rope_cos; qp.rope_sin = rope_sin;
+    if ((rc = launch_qkv_post(qp, stream))) return rc;
+    AttnArgs at;
+    at.q = pf_q; at.ldq = qd; at.kc = kc; at.vc = vc; at.kv_type = desc.kv_type;
+    at.o = pf_att; at.ldo = qd; at.nq = nq; at.nkv = nkv; at.hd = hd; at.L_stride = mc;
+    at.L_host = p0 + 1; at.nqb = T; at.n_chunks = nch; at.chunk_len = cl; at.part = pf_part;
+    if ((rc = launch_attn_decode(at, stream))) return rc;
+    if ((rc = prep(pf_att, nullptr, qd, nullptr)) || (rc = gemm(L.o, qd, H, pf_x, H, pf_x))) return rc;
+    if ((rc = prep(pf_x, nullptr, H, L.ffn_norm)) || (rc = gemm(L.gate, H, F, pf_g, F, nullptr)) ||
+        (rc = gemm(L.up, H, F, pf_u, F, nullptr)))
+      return rc;
+    if ((rc = prep(pf_g, pf_u, F, nullptr)) || (rc = gemm(L.down, F, H, pf_x, H, pf_x))) return rc;
+  }
+  return TPT_OK;
+}
+
+// Layers [l0, l1) on caller-given residual rows (x_in, host [n][embed]) at positions pos0 ..,
+// through the batched kernels (path 0) or one decode-step layer stack per position (path 1);
+// the layers' K/V rows at those positions are written as a forward pass writes them.
+int tpt_model::run_layers(const float* x_in, int n, int pos0, int l0, int l1, int path, float* x_out) {
+  const int H = desc.embed;
+  if (n <= 0 || pos0 < 0 || pos0 + n > desc.max_ctx || l0 < 0 || l1 > desc.n_layers || l0 > l1 ||
+      (path != 0 && path != 1))
+    return fail(TPT_ERR_INVALID, "run_layers: bad range or path");
+  if (path == 0 && !batched_prefill) return fail(TPT_ERR_UNSUPPORTED, "run_layers: batched path needs Q4_K layer matrices");
+  int rc;
+  if (path == 0) {
+    for (int c0 = 0; c0 < n; c0 += kPrefillT) {
+      const int T = std::min(kPrefillT, n - c0), p0 = pos0 + c0;
+      if ((rc = prefill_scratch(T, slice_chunks(p0 + T)))) return rc;
+      TPT_HIP(hipMemcpyAsync(pf_x, x_in + (size_t)c0 * H, (size_t)T * H * 4, hipMemcpyHostToDevice, stream));
+      if ((rc = batched_layers(T, p0, l0, l1))) return rc;
+      TPT_HIP(hipMemcpyAsync(x_out + (size_t)c0 * H, pf_x, (size_t)T * H * 4, hipMemcpyDeviceToHost, stream));
+      TPT_HIP(hipStreamSynchronize(stream));
+    }
+    return TPT_OK;
+  }
+  for (int t = 0; t < n; t++) {
+    const int p = pos0 + t, bucket = bucket_of(p + 1);
+    const int nch = std::min(attn_default_chunks(bucket, desc.n_kv_heads), attn_max_chunks);
+    memset(st_host, 0, sizeof(StepState));
+    st_host->pos = p;
+    st_host->next_pos = p + 1;
+    TPT_HIP(hipMemcpyAsync(st, st_host, sizeof(StepState), hipMemcpyHostToDevice, stream));
+    TPT_HIP(hipMemcpyAsync(x, x_in + (size_t)t * H, (size_t)H * 4, hipMemcpyHostToDevice, stream));
+    for (int l = l0; l < l1; l++)
+      if ((rc = enqueue_layer(l, nch, attn_chunk_len(bucket, nch)))) return rc;
+    TPT_HIP(hipMemcpyAsync(x_out + (size_t)t * H, x, (size_t)H * 4, hipMemcpyDeviceToHost, stream));
+    TPT_HIP(hipStreamSynchronize(stream));
   }
   return TPT_OK;
 }
@@ -755,6 +810,27 @@ int tpt_model_decode_greedy(tpt_model* m, uint32_t first, int pos0, int n_steps,
   int rc = ctx_enter(m->ctx);
   if (rc) return rc;
   return m->decode_greedy(first, pos0, n_steps, stop_token, tokens_out);
+}
+
+int tpt_model_run_layers(tpt_model* m, const float* x_in, int n, int pos0, int l0, int l1, int path,
+                         float* x_out) {
+  if (!m || !x_in || !x_out) return fail(TPT_ERR_INVALID, "null argument");
+  int rc = ctx_enter(m->ctx);
+  if (rc) return rc;
+  return m->run_layers(x_in, n, pos0, l0, l1, path, x_out);
+}
+
+int tpt_model_kv_read(tpt_model* m, int layer, void* k_host, void* v_host) {
+  if (!m || !k_host || !v_host) return fail(TPT_ERR_INVALID, "null argument");
+  if (layer < 0 || layer >= m->desc.n_layers) return fail(TPT_ERR_INVALID, "kv_read: layer out of range");
+  int rc = ctx_enter(m->ctx);
+  if (rc) return rc;
+  const size_t half = (size_t)m->desc.n_kv_heads * m->desc.max_ctx * m->desc.head_dim * m->kv_elem;
+  const uint8_t* kc = (const uint8_t*)m->kv + (size_t)layer * 2 * half;
+  TPT_HIP(hipMemcpyAsync(k_host, kc, half, hipMemcpyDeviceToHost, m->stream));
+  TPT_HIP(hipMemcpyAsync(v_host, kc + half, half, hipMemcpyDeviceToHost, m->stream));
+  TPT_HIP(hipStreamSynchronize(m->stream));
+  return TPT_OK;
 }
 
 int tpt_model_hidden(tpt_model* m, float* out_host) {

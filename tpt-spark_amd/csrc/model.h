@@ -64,6 +64,7 @@ struct tpt_model {
   int load(tpt_ctx* c, const char* gguf_path, int max_ctx, int kv_type, tpt_progress_fn progress,
            void* user);
   int enqueue_step(int bucket, bool lm_head);
+  int enqueue_layer(int l, int n_chunks, int chunk_len);
   int launch_step(int L, bool lm_head);  // graph replay (or direct launches)
   int bucket_of(int L) const;
   int set_state(int next_pos, int prompt_len, int use_override, uint32_t tok);
@@ -72,6 +73,8 @@ struct tpt_model {
   int prefill_steps(int n, int pos0);       // one decode step per position
   int prefill_batched(int n, int pos0);     // GEMM path; ids already in ids_host
   int prefill_scratch(int T, int n_chunks);
+  int batched_layers(int T, int p0, int l0, int l1);  // layers [l0, l1) over the rows in pf_x
+  int run_layers(const float* x_in, int n, int pos0, int l0, int l1, int path, float* x_out);
   // fn(user, s, tok) receives the token step s produced, in order; non-zero stops the run.
   typedef int (*StepFn)(void* user, int s, uint32_t tok);
   int decode_stream(uint32_t first, int pos0, int n_steps, StepFn fn, void* user, int* n_delivered);

@@ -44,6 +44,16 @@ __device__ __forceinline__ uint16_t f2h(float f) {
   return __builtin_bit_cast(uint16_t, (_Float16)f);  // round to nearest even
 }
 
+// candle's silu(g) * u: g / (1 + exp(-g)) in f32 (correctly rounded divide), times u.  exp(-g)
+// is the f64 exponential rounded once to f32, i.e. the correctly rounded f32 value, which the
+// host libm's expf returns for all but a vanishing fraction of arguments (its error bound is a
+// hair above half an ulp); the device's single-precision expf differs from it in the last place
+// for about 3% of arguments.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  const float e = (float)exp(-(double)g);
+  return g / (1.f + e) * u;
+}
+
 template <typename T>
 __device__ __forceinline__ T ldg_u(const uint8_t* p) {  // unaligned-tolerant load
   T v;

@@ -8,6 +8,7 @@ a missing library raises at import of the first call.
 """
 import ctypes as C
 import os
+import weakref
 from dataclasses import dataclass, field
 from typing import Callable, List, Optional
 
@@ -73,6 +74,7 @@ EXPORTS = {
     "tpt_dequant": ([P, I32, P, P, I64], I32),
     "tpt_gemv": ([P, I32, P, P, P, I32, I32, I32], I32),
     "tpt_gemv_rmsnorm": ([P, I32, P, P, P, F32, P, I32, I32], I32),
+    "tpt_swiglu": ([P, P, P, P, I32], I32),
     "tpt_rmsnorm": ([P, P, P, P, I32, F32], I32),
     "tpt_rope": ([P, P, I32, I32, I32, P, P], I32),
     "tpt_attn_decode": ([P, P, P, P, I32, P, I32, I32, I32, I32, I32, I32], I32),
@@ -84,6 +86,8 @@ EXPORTS = {
     "tpt_model_decode_step": ([P, U32, I32, P, P], I32),
     "tpt_model_decode_greedy": ([P, U32, I32, I32, I64, P], I32),
     "tpt_model_hidden": ([P, P], I32),
+    "tpt_model_run_layers": ([P, P, I32, I32, I32, I32, I32, P], I32),
+    "tpt_model_kv_read": ([P, I32, P, P], I32),
     "tpt_engine_create": ([I32, P], I32),
     "tpt_engine_set_kv_type": ([P, I32], I32),
     "tpt_engine_destroy": ([P], I32),
@@ -150,10 +154,11 @@ class DeviceBuffer:
     """A device allocation owned by a Context."""
 
     def __init__(self, ctx, nbytes):
-        self.ctx, self.nbytes = ctx, int(nbytes)
+        self.ctx, self.nbytes, self.ptr = ctx, int(nbytes), None
         p = C.c_void_p()
         check(lib().tpt_malloc(ctx.h, self.nbytes, C.byref(p)))
         self.ptr = p.value
+        ctx._children.add(self)
 
     def upload(self, arr):
         arr = np.ascontiguousarray(arr)
@@ -173,9 +178,9 @@ class DeviceBuffer:
         return self
 
     def free(self):
-        if self.ptr:
+        if self.ptr and self.ctx.h:
             lib().tpt_free(self.ctx.h, self.ptr)
-            self.ptr = None
+        self.ptr = None
 
     def __del__(self):
         try:
@@ -188,6 +193,8 @@ class Context:
     """One device and one HIP stream (tpt_ctx)."""
 
     def __init__(self, device=0):
+        self.h = None
+        self._children = weakref.WeakSet()  # buffers and models, released before the context
         h = C.c_void_p()
         check(lib().tpt_ctx_create(device, C.byref(h)))
         self.h = h.value
@@ -198,8 +205,16 @@ class Context:
 
     def close(self):
         if self.h:
+            for c in list(self._children):
+                c.close() if isinstance(c, Model) else c.free()
             lib().tpt_ctx_destroy(self.h)
             self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
     def synchronize(self):
         check(lib().tpt_ctx_synchronize(self.h))
@@ -230,6 +245,11 @@ class Context:
     def rmsnorm(self, xbuf, wbuf, n, eps):
         y = self.alloc(n * 4)
         check(lib().tpt_rmsnorm(self.h, xbuf.ptr, wbuf.ptr, y.ptr, n, eps))
+        return y.download(np.float32, n)
+
+    def swiglu(self, gbuf, ubuf, n):
+        y = self.alloc(n * 4)
+        check(lib().tpt_swiglu(self.h, gbuf.ptr, ubuf.ptr, y.ptr, n))
         return y.download(np.float32, n)
 
     def rope(self, xbuf, n_heads, hd, pos, cosbuf, sinbuf):
@@ -287,21 +307,22 @@ class Model:
     """tpt_model: a GGUF resident in HBM with its KV cache (fp16, or f32 like candle's)."""
 
     def __init__(self, ctx, path, max_ctx=0, on_progress=None, kv_type=TYPE_F16):
-        self.ctx = ctx
+        self.ctx, self.h = ctx, None
         self._cb = PROGRESS_FN(lambda u, d, t: on_progress(d, t)) if on_progress else PROGRESS_FN()
         h = C.c_void_p()
         check(lib().tpt_model_load(ctx.h, path.encode(), max_ctx, kv_type, self._cb, None,
                                    C.byref(h)))
         self.h = h.value
+        ctx._children.add(self)
         d = ModelDesc()
         check(lib().tpt_model_describe(self.h, C.byref(d)))
         self.desc = {n: getattr(d, n) for n, _ in ModelDesc._fields_}
         self.desc["architecture"] = d.architecture.decode()
 
     def close(self):
-        if self.h:
+        if self.h and self.ctx.h:
             lib().tpt_model_destroy(self.h)
-            self.h = None
+        self.h = None
 
     def __del__(self):
         try:
@@ -331,6 +352,25 @@ class Model:
     def hidden(self):
         out = np.empty(self.desc["embed"], np.float32)
         check(lib().tpt_model_hidden(self.h, _ptr(out)))
+        return out
+
+    PATH_BATCHED, PATH_STEPS = 0, 1
+
+    def kv(self, layer):
+        """Layer's K and V caches as float32 arrays [n_kv_heads, max_ctx, head_dim]."""
+        d = self.desc
+        shape = (d["n_kv_heads"], d["max_ctx"], d["head_dim"])
+        dt = np.float32 if d["kv_type"] == TYPE_F32 else np.float16
+        k, v = np.empty(shape, dt), np.empty(shape, dt)
+        check(lib().tpt_model_kv_read(self.h, layer, _ptr(k), _ptr(v)))
+        return k.astype(np.float32), v.astype(np.float32)
+
+    def run_layers(self, x, pos0, l0, l1, path=0):
+        """Decoder layers [l0, l1) on residual rows x [n, embed] at positions pos0 ..; returns
+        the output rows.  path 0: batched prefill kernels, 1: decode-step kernels."""
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, self.desc["embed"])
+        out = np.empty_like(x)
+        check(lib().tpt_model_run_layers(self.h, _ptr(x), x.shape[0], pos0, l0, l1, path, _ptr(out)))
         return out
 
 
