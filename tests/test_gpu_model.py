@@ -24,6 +24,12 @@ def kv(request):
 
 KV_TYPE = {"f16": tpthip.TYPE_F16, "f32": tpthip.TYPE_F32}
 
+# fp16 K/V rounding can flip under f32 summation-order differences, and a flipped K/V entry
+# feeds every later position: over a 150-token prompt the oracle itself moves by 0.011 (block-
+# reduced dot products) to 0.013 (fused-multiply-add attention) in max-abs logits with the fp16
+# cache, and by 2e-7 with the f32 cache.  Logit bars in the fp16 mode are set to that spread.
+FP16_LOGIT_TOL = 4e-2
+
 
 @pytest.fixture(scope="module")
 def tiny_model(ctx, tiny_gguf, kv):
@@ -59,21 +65,24 @@ def test_prefill_logits_match_oracle(tiny_model, tiny_oracle, kv):
 
 
 def test_greedy_tokens_match_oracle(tiny_model, tiny_oracle, kv):
-    """40 greedy tokens identical to the oracle in the same cache mode; for the f32 cache that
-    is candle's greedy sequence (the bar: the first 32 identical, logits within 1e-2)."""
+    """Greedy tokens identical to the oracle in the same cache mode: the first 32 (the bar; for
+    the f32 cache that is candle's greedy sequence) and, with the f32 cache, all 40.  An fp16
+    cache entry can round the other way under an f32 summation-order difference, and such a flip
+    can move a later token, so past the bar the fp16 mode is not held to identity."""
     n = 40
     toks_ref, logits_ref = tiny_oracle.greedy(PROMPT, n, kv_f16=(kv == "f16"), return_logits=(1, 32))
     first = tiny_model.prefill(PROMPT, 0)
     got = [first] + tiny_model.decode_greedy(first, len(PROMPT), n - 1)
     assert got[:32] == toks_ref[:32]
-    assert got == toks_ref
+    if kv == "f32":
+        assert got == toks_ref
     # logits of a later step through the single-step path
     pos = len(PROMPT)
     tiny_model.prefill(PROMPT, 0)
     for i in range(31):
         tiny_model.decode_step(got[i], pos + i)
     _, lg = tiny_model.decode_step(got[31], pos + 31, logits=True)
-    assert np.abs(lg - logits_ref[32]).max() < 1e-2
+    assert np.abs(lg - logits_ref[32]).max() < (1e-2 if kv == "f32" else FP16_LOGIT_TOL)
 
 
 def test_graph_decode_equals_stepwise(tiny_model):
@@ -253,11 +262,7 @@ def test_load_errors(ctx, tiny_gguf, tmp_path):
 
 # ---------------------------------------------------------------- batched prefill
 
-# fp16 K/V rounding can flip under f32 summation-order differences, and a flipped K/V entry
-# feeds every later position: over a 150-token prompt the oracle itself moves by 0.011 (block-
-# reduced dot products) to 0.013 (fused-multiply-add attention) in max-abs logits with the fp16
-# cache, and by 2e-7 with the f32 cache.
-LONG_TOL = {"f32": 1e-3, "f16": 4e-2}
+LONG_TOL = {"f32": 1e-3, "f16": FP16_LOGIT_TOL}
 
 
 def test_batched_prefill_equals_steps(ctx, tiny_gguf, kv):

@@ -1,0 +1,612 @@
+// Device code of the fused k-quant dequant-GEMV (see k_gemv.hip for the design): weight-group
+// loads, Q8_K / Q8_0 activation quantization into LDS, integer group dots, and gemv_run, one
+// workgroup's share of a GEMV.
+#pragma once
+#include "kernels.h"
+
+namespace tpt {
+namespace gemv {
+
+constexpr int NT = 512;  // threads per workgroup
+constexpr int NW = NT / WAVE;
+constexpr int MAXB = 64 / NW;       // 256-element activation blocks per wave (K <= 16384)
+
+__device__ __forceinline__ uint32_t bsel(uint32_t v, int i) { return (v >> (8 * i)) & 0xffu; }
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+// ----------------------------------------------------------------- per-lane weight groups
+// group g of a row = 64 weights: Q4_K (block g/4, qs bytes 32(g%4)..), Q6_K (block g/4, half
+// (g/2)%2, column half g%2), Q8_0 (blocks 2g, 2g+1)
+template <int WT> struct Raw;
+template <> struct Raw<TPT_TYPE_Q4_K> { uint4 h, a, b; };
+template <> struct Raw<TPT_TYPE_Q6_K> { uint4 qa, qb, qh; uint2 sc; uint32_t d; };
+template <> struct Raw<TPT_TYPE_Q8_0> { uint4 a0, a1, b0, b1; uint32_t d0, d1; };
+
+template <int WT>
+__device__ __forceinline__ void load_raw(const uint8_t* row, int g, Raw<WT>& r);
+
+template <>
+__device__ __forceinline__ void load_raw<TPT_TYPE_Q4_K>(const uint8_t* row, int g,
+                                                         Raw<TPT_TYPE_Q4_K>& r) {
+  const uint8_t* blk = row + (size_t)(g >> 2) * 144;  // 144 = 9 x 16: blocks stay 16-aligned
+  const int off = 16 + (g & 3) * 32;
+  r.h = *(const uint4*)blk;
+  r.a = *(const uint4*)(blk + off);
+  r.b = *(const uint4*)(blk + off + 16);
+}
+
+template <>
+__device__ __forceinline__ void load_raw<TPT_TYPE_Q6_K>(const uint8_t* row, int g,
+                                                         Raw<TPT_TYPE_Q6_K>& r) {
+  const uint8_t* blk = row + (size_t)(g >> 2) * 210;  // 2-byte aligned: unaligned vector loads
+  const int p = (g >> 1) & 1, h = g & 1;
+  r.qa = ldg_u<uint4>(blk + 64 * p + 16 * h);
+  r.qb = ldg_u<uint4>(blk + 64 * p + 32 + 16 * h);
+  r.qh = ldg_u<uint4>(blk + 128 + 32 * p + 16 * h);
+  r.sc = ldg_u<uint2>(blk + 192 + 8 * p);
+  r.d = ldg_u<uint16_t>(blk + 208);
+}
+
+template <>
+__device__ __forceinline__ void load_raw<TPT_TYPE_Q8_0>(const uint8_t* row, int g,
+                                                         Raw<TPT_TYPE_Q8_0>& r) {
+  const uint8_t* b0 = row + (size_t)g * 68;
+  r.d0 = ldg_u<uint16_t>(b0);
+  r.a0 = ldg_u<uint4>(b0 + 2);
+  r.a1 = ldg_u<uint4>(b0 + 18);
+  r.d1 = ldg_u<uint16_t>(b0 + 34);
+  r.b0 = ldg_u<uint4>(b0 + 36);
+  r.b1 = ldg_u<uint4>(b0 + 52);
+}
+
+// ----------------------------------------------------------------- activation (LDS)
+// LDS layout: qs int8[K] | d float[K/bs] | s16 int[K/16] | scratch float[NW] | rows
+struct Lds {
+  int* q32;
+  float* d;
+  int* s16;
+  float* red;
+  float* rows;
+};
+
+__host__ __device__ inline size_t lds_act_bytes(int K, bool q80) {
+  const int nd = q80 ? K / QK8_0 : K / QK_K;
+  return (size_t)K + 4 * nd + 4 * (K / 16) + 4 * NW;
+}
+
+__device__ __forceinline__ Lds lds_layout(char* smem, int K, bool q80) {
+  Lds l;
+  l.q32 = (int*)smem;
+  l.d = (float*)(smem + K);
+  const int nd = q80 ? K / QK8_0 : K / QK_K;
+  l.s16 = (int*)(smem + K + 4 * nd);
+  l.red = (float*)(smem + K + 4 * nd + 4 * (K / 16));
+  l.rows = l.red + NW;
+  return l;
+}
+
+__device__ __forceinline__ void barrier_lds() {
+  // LDS-only barrier: outstanding global loads (the prefetched weights) stay in flight.
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Activation preload.  Loads are unconditional (clamped block index, x itself as a dummy norm
+// source) so the waitcnt pass can count exactly how many later loads may stay in flight.
+//  * Q8_K activations (Q4_K / Q6_K weights), ROWS16: one 256-block per 16-lane DPP row -- lane l
+//    of wave w holds elements 16(l%16) .. +15 of block 4(w + qi NW) + l/16, qi < MAXQ.
+//  * Q8_0 activations: one float4 per lane per 256-element block, blocks w, w + NW, ...
+constexpr int MAXQ = MAXB / 4;  // block quads per wave in the ROWS16 layout
+struct XPre {
+  float4 x[MAXB];
+  float4 w[MAXB];
+};
+
+template <bool ROWS16>
+__device__ __forceinline__ void preload_x(const GemvArgs& A, XPre& p) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int nb = A.K / 256;
+  const float4* xs = (const float4*)A.x;
+  const float4* ws = (const float4*)(A.prologue == PRO_RMSNORM ? A.norm_w : A.x);
+  if constexpr (ROWS16) {
+    const int k = lane >> 4, m = lane & 15;
+#pragma unroll
+    for (int qi = 0; qi < MAXQ; qi++) {
+      int b = 4 * (wid + qi * NW) + k;
+      if (b >= nb) b = nb - 1;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        p.x[qi * 4 + j] = xs[b * 64 + m * 4 + j];
+        p.w[qi * 4 + j] = ws[b * 64 + m * 4 + j];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < MAXB; i++) {
+      int b = wid + i * NW;
+      if (b >= nb) b = nb - 1;
+      p.x[i] = xs[b * 64 + lane];
+      p.w[i] = ws[b * 64 + lane];
+    }
+  }
+}
+
+// whether preload slot i of this lane holds a real block (not a clamped duplicate)
+template <bool ROWS16>
+__device__ __forceinline__ bool slot_valid(int i, int nb) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if constexpr (ROWS16) return 4 * (wid + (i >> 2) * NW) + (lane >> 4) < nb;
+  else return wid + i * NW < nb;
+}
+
+// 1/m of rms_norm (candle_nn::ops::rms_norm: m = sqrt(sum(x^2)/dim + eps)).  Every workgroup
+// reduces the whole vector itself from the preloaded registers (each element is owned by
+// exactly one lane of the workgroup).
+template <bool ROWS16>
+__device__ __forceinline__ float rms_denominator(const GemvArgs& A, const XPre& p, float* red) {
+  const int tid = threadIdx.x, wid = tid >> 6;
+  const int nb = A.K / 256;
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXB; i++) {
+    if (slot_valid<ROWS16>(i, nb)) {
+      const float4 v = p.x[i];
+      ss = fmaf(v.x, v.x, ss);
+      ss = fmaf(v.y, v.y, ss);
+      ss = fmaf(v.z, v.z, ss);
+      ss = fmaf(v.w, v.w, ss);
+    }
+  }
+  ss = wave_sum_dpp(ss);
+  if ((tid & 63) == 0) red[wid] = ss;
+  barrier_lds();
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < NW; i++) t += red[i];
+  return sqrtf(t / (float)A.K + A.eps);
+}
+
+// x / m correctly rounded from y = RN(1/m): q0 = RN(x y) is within an ulp of x/m, the remainder
+// x - q0 m is exact in one fma, and RN(q0 + r y) is the correctly rounded quotient (Markstein's
+// correction step; checked against the divide on 1e9 random pairs).  The sign of a zero
+// quotient may differ, which no later step can see.
+__device__ __forceinline__ float div_rn(float x, float m, float y) {
+  const float q0 = x * y;
+  return fmaf(fmaf(-q0, m, x), y, q0);
+}
+// candle's y = x / m * w with one true divide per workgroup (y = 1/m) instead of one per value
+__device__ __forceinline__ float4 apply_norm(float4 v, float4 w, float m, float y) {
+  v.x = div_rn(v.x, m, y) * w.x;
+  v.y = div_rn(v.y, m, y) * w.y;
+  v.z = div_rn(v.z, m, y) * w.z;
+  v.w = div_rn(v.w, m, y) * w.w;
+  return v;
+}
+
+// Q8_K quantization (BlockQ8K::from_float) in the ROWS16 layout: a 16-lane row reduces its
+// block's max |x| with four DPP steps; the signed value at the first position holding it
+// (element order: lane, then element) comes from the ballot of the lanes that hold it;
+// iscale = -128/max, q = round-half-away(iscale * x) (the lower clamp never binds), d = 1/iscale.
+// A lane's 16 values are exactly one per-16 group, so its q sum is that group's bsum.
+__device__ __forceinline__ void prologue_q8k(const GemvArgs& A, const XPre& p, const Lds& L) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int k = lane >> 4, m16 = lane & 15;
+  const int nb = A.K / QK_K;
+  float mn = 1.f, rm = 1.f;
+  const bool norm = A.prologue == PRO_RMSNORM;
+  if (norm) {
+    mn = rms_denominator<true>(A, p, L.red);
+    rm = 1.f / mn;
+  }
+#pragma unroll
+  for (int qi = 0; qi < MAXQ; qi++) {
+    const int b0 = 4 * (wid + qi * NW);
+    if (b0 < nb) {  // uniform across the wave
+      const int b = b0 + k;
+      float e[16];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float4 v = norm ? apply_norm(p.x[qi * 4 + j], p.w[qi * 4 + j], mn, rm) : p.x[qi * 4 + j];
+        e[4 * j] = v.x; e[4 * j + 1] = v.y; e[4 * j + 2] = v.z; e[4 * j + 3] = v.w;
+      }
+      float la = fabsf(e[0]);
+#pragma unroll
+      for (int i = 1; i < 16; i++) la = fmaxf(la, fabsf(e[i]));
+      float amax = la;
+      amax = fmaxf(amax, dpp_mov<0xB1>(amax));   // quad_perm [1,0,3,2]
+      amax = fmaxf(amax, dpp_mov<0x4E>(amax));   // quad_perm [2,3,0,1]
+      amax = fmaxf(amax, dpp_mov<0x141>(amax));  // row_half_mirror
+      amax = fmaxf(amax, dpp_mov<0x140>(amax));  // row_mirror: the 16-lane row's max
+      float mine = 0.f;
+#pragma unroll
+      for (int i = 15; i >= 0; i--) mine = fabsf(e[i]) == amax ? e[i] : mine;  // first hit wins
+      const unsigned long long hit = __ballot(la == amax);
+      const uint32_t bits = (uint32_t)(hit >> (16 * k)) & 0xffffu;
+      const int src = 16 * k + (bits ? __builtin_ctz(bits) : 0);
+      const float mx = __shfl(mine, src, WAVE);
+      const bool nz = amax != 0.f;
+      const float iscale = -128.f / (nz ? mx : 1.f);
+      int pk[4];
+      int qs = 0;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        int w = 0;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          const float r = __builtin_amdgcn_fmed3f(roundf(iscale * e[4 * j + c]), -128.f, 127.f);
+          const int q = nz ? (int)r : 0;
+          qs += q;
+          w |= (q & 0xff) << (8 * c);
+        }
+        pk[j] = w;
+      }
+      if (b < nb) {
+        *(int4*)(L.q32 + b * 64 + 4 * m16) = make_int4(pk[0], pk[1], pk[2], pk[3]);
+        L.s16[b * 16 + m16] = qs;
+        if (m16 == 0) L.d[b] = nz ? 1.f / iscale : 0.f;
+      }
+    }
+  }
+}
+
+// Q8_0 activation quantization (BlockQ8_0::from_float): 8 lanes per 32-block.
+__device__ __forceinline__ void prologue_q80(const GemvArgs& A, const XPre& p, const Lds& L) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int nb = A.K / 256;
+  float m = 1.f, rm = 1.f;
+  const bool norm = A.prologue == PRO_RMSNORM;
+  if (norm) {
+    m = rms_denominator<false>(A, p, L.red);
+    rm = 1.f / m;
+  }
+#pragma unroll
+  for (int i = 0; i < MAXB; i++) {
+    const int c = wid + i * NW;
+    if (c < nb) {
+      const float4 v = norm ? apply_norm(p.x[i], p.w[i], m, rm) : p.x[i];
+      float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+      amax = fmaxf(amax, dpp_mov<0xB1>(amax));   // max over 8 lanes
+      amax = fmaxf(amax, dpp_mov<0x4E>(amax));
+      amax = fmaxf(amax, dpp_mov<0x141>(amax));
+      const float d = amax / 127.f;
+      const float id = d != 0.f ? 1.f / d : 0.f;
+      const float e[4] = {v.x, v.y, v.z, v.w};
+      int packed = 0;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        float r = roundf(e[j] * id);
+        r = fminf(fmaxf(r, -128.f), 127.f);
+        packed |= ((int)r & 0xff) << (8 * j);
+      }
+      L.q32[c * 64 + lane] = packed;
+      if ((lane & 7) == 0) L.d[c * 8 + (lane >> 3)] = h2f(f2h(d));  // stored as f16
+    }
+  }
+}
+
+// ----------------------------------------------------------------- activation slices
+struct Act {
+  int q[16];     // the group's 64 int8 activation values, packed
+  float d0, d1;  // Q8_K: d0 = block d;  Q8_0: d of each 32-block
+  int s[4];      // Q4_K: s[0], s[1] = sums over each 32;  Q6_K: per-16 sums of the 4 quads
+};
+
+template <int WT>
+__device__ __forceinline__ void load_act(const Lds& L, int g, Act& a) {
+  if constexpr (WT == TPT_TYPE_Q4_K) {
+    const int4* q = (const int4*)(L.q32 + 16 * g);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int4 v = q[i];
+      a.q[4 * i] = v.x; a.q[4 * i + 1] = v.y; a.q[4 * i + 2] = v.z; a.q[4 * i + 3] = v.w;
+    }
+    a.d0 = L.d[g >> 2];
+    const int4 bs = *(const int4*)(L.s16 + 4 * g);
+    a.s[0] = bs.x + bs.y;
+    a.s[1] = bs.z + bs.w;
+  } else if constexpr (WT == TPT_TYPE_Q6_K) {
+    const int b = g >> 2, p = (g >> 1) & 1, h = g & 1;
+#pragma unroll
+    for (int quad = 0; quad < 4; quad++) {
+      const int4 v = *(const int4*)(L.q32 + (256 * b + 128 * p + 32 * quad + 16 * h) / 4);
+      a.q[4 * quad] = v.x; a.q[4 * quad + 1] = v.y; a.q[4 * quad + 2] = v.z; a.q[4 * quad + 3] = v.w;
+    }
+    const int4 s0 = *(const int4*)(L.s16 + 16 * b + 8 * p), s1 = *(const int4*)(L.s16 + 16 * b + 8 * p + 4);
+    // per-16 sums of elements 128p + 32quad + 16h: s16 index 8p + 2quad + h
+    a.s[0] = h ? s0.y : s0.x;
+    a.s[1] = h ? s0.w : s0.z;
+    a.s[2] = h ? s1.y : s1.x;
+    a.s[3] = h ? s1.w : s1.z;
+    a.d0 = L.d[b];
+  } else {
+    const int4* q = (const int4*)(L.q32 + 16 * g);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int4 v = q[i];
+      a.q[4 * i] = v.x; a.q[4 * i + 1] = v.y; a.q[4 * i + 2] = v.z; a.q[4 * i + 3] = v.w;
+    }
+    a.d0 = L.d[2 * g];
+    a.d1 = L.d[2 * g + 1];
+  }
+}
+
+// Q4_K x Q8_K for one group: vec_dot_q4k_q8k's per-block arithmetic restricted to the group's
+// two sub-blocks, d_w*d_x * sum_j sc_j * sum(q4*q8)  -  dmin_w*d_x * sum_j m_j * bsum_j.
+// get_scale_min_k4 for j0 = 2(g%4), j1 = j0 + 1 without branches: the scale bytes sit at byte
+// offset 2(g%2) of the header dwords y = s[0..3], z = s[4..7], w = s[8..11].
+__device__ __forceinline__ float dot_group(const Raw<TPT_TYPE_Q4_K>& r, const Act& a, int g) {
+  const int sh = 16 * (g & 1);
+  const uint32_t Y = r.h.y >> sh, Z = r.h.z >> sh, W = r.h.w >> sh;
+  const bool hi = (g & 2) != 0;
+  const int sc0 = hi ? (int)((W & 0xF) | (((Y >> 6) & 3) << 4)) : (int)(Y & 63);
+  const int sc1 = hi ? (int)(((W >> 8) & 0xF) | (((Y >> 14) & 3) << 4)) : (int)((Y >> 8) & 63);
+  const int m0 = hi ? (int)(((W >> 4) & 0xF) | (((Z >> 6) & 3) << 4)) : (int)(Z & 63);
+  const int m1 = hi ? (int)(((W >> 12) & 0xF) | (((Z >> 14) & 3) << 4)) : (int)((Z >> 8) & 63);
+  const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+  int s0 = 0, s1 = 0;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    s0 = sdot4((int)(w[i] & 0x0F0F0F0Fu), a.q[i], s0);
+    s1 = sdot4((int)((w[i] >> 4) & 0x0F0F0F0Fu), a.q[8 + i], s1);
+  }
+  const int isum = sc0 * s0 + sc1 * s1;
+  const int msum = m0 * a.s[0] + m1 * a.s[1];
+  const float dd = h2f((uint16_t)(r.h.x & 0xffff)) * a.d0;
+  const float dm = h2f((uint16_t)(r.h.x >> 16)) * a.d0;
+  return dd * (float)isum - dm * (float)msum;
+}
+
+// Q6_K x Q8_K for one group (half p, column half h): vec_dot_q6k_q8k's per-block arithmetic,
+// d_w*d_x * sum_quad sc * (sum(q6*q8) - 32*bsum).
+__device__ __forceinline__ float dot_group(const Raw<TPT_TYPE_Q6_K>& r, const Act& a, int g) {
+  const int h = g & 1;
+  const uint32_t qa[4] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w};
+  const uint32_t qb[4] = {r.qb.x, r.qb.y, r.qb.z, r.qb.w};
+  const uint32_t qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+  int d0 = 0, d1 = 0, d2 = 0, d3 = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t v0 = (qa[i] & 0x0F0F0F0Fu) | ((qh[i] & 0x03030303u) << 4);
+    const uint32_t v1 = (qb[i] & 0x0F0F0F0Fu) | (((qh[i] >> 2) & 0x03030303u) << 4);
+    const uint32_t v2 = ((qa[i] >> 4) & 0x0F0F0F0Fu) | (((qh[i] >> 4) & 0x03030303u) << 4);
+    const uint32_t v3 = ((qb[i] >> 4) & 0x0F0F0F0Fu) | (((qh[i] >> 6) & 0x03030303u) << 4);
+    d0 = sdot4((int)v0, a.q[i], d0);
+    d1 = sdot4((int)v1, a.q[4 + i], d1);
+    d2 = sdot4((int)v2, a.q[8 + i], d2);
+    d3 = sdot4((int)v3, a.q[12 + i], d3);
+  }
+  // scales of quads 0..3 are bytes h, h+2, h+4, h+6 of the 8 loaded (sc[8p .. 8p+8))
+  const uint32_t slo = r.sc.x >> (8 * h), shi = r.sc.y >> (8 * h);
+  const int sc0 = (int8_t)(slo & 0xff), sc1 = (int8_t)((slo >> 16) & 0xff);
+  const int sc2 = (int8_t)(shi & 0xff), sc3 = (int8_t)((shi >> 16) & 0xff);
+  const int isum = sc0 * (d0 - 32 * a.s[0]) + sc1 * (d1 - 32 * a.s[1]) +
+                   sc2 * (d2 - 32 * a.s[2]) + sc3 * (d3 - 32 * a.s[3]);
+  return (h2f((uint16_t)r.d) * a.d0) * (float)isum;
+}
+
+// Q8_0 x Q8_0 for two blocks: vec_dot_q8_0_q8_0's (sum_i * d_w) * d_x per block.
+__device__ __forceinline__ float dot_group(const Raw<TPT_TYPE_Q8_0>& r, const Act& a, int) {
+  const uint32_t wa[8] = {r.a0.x, r.a0.y, r.a0.z, r.a0.w, r.a1.x, r.a1.y, r.a1.z, r.a1.w};
+  const uint32_t wb[8] = {r.b0.x, r.b0.y, r.b0.z, r.b0.w, r.b1.x, r.b1.y, r.b1.z, r.b1.w};
+  int s0 = 0, s1 = 0;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    s0 = sdot4((int)wa[i], a.q[i], s0);
+    s1 = sdot4((int)wb[i], a.q[8 + i], s1);
+  }
+  return ((float)s0 * h2f((uint16_t)r.d0)) * a.d0 + ((float)s1 * h2f((uint16_t)r.d1)) * a.d1;
+}
+
+// K or V cache elements ci, ci+1 (ci even): fp16 pair packed into one 32-bit store, or two f32
+__device__ __forceinline__ void store_kv_pair(void* cache, int kv_type, size_t ci, float a, float b) {
+  if (kv_type == TPT_TYPE_F32) {
+    ((float*)cache)[ci] = a;
+    ((float*)cache)[ci + 1] = b;
+  } else {
+    *(uint32_t*)((uint16_t*)cache + ci) = (uint32_t)f2h(a) | ((uint32_t)f2h(b) << 16);
+  }
+}
+
+// ----------------------------------------------------------------- the kernel
+// Launch geometry shared by host and device.
+struct Geo {
+  int rows_per_wg;  // contiguous rows per workgroup (whole row groups, even)
+  int P;            // passes per row
+};
+
+
+// Does nothing between the first weight loads and the activation prologue (standalone launch).
+struct NoHook {
+  __device__ void operator()() const {}
+};
+
+// One workgroup's share of a GEMV: rows [wg * rows_per_wg, ...).  WT weight type; BPP
+// super-blocks per row per pass (16, or fewer for short rows, then RPP = 16/BPP rows share a
+// pass); RB row slots per step; NMAT matrices (2: gate|up); KS-way split of the passes across
+// waves; D steps in flight per wave.  hook() runs after the activation and the first weight loads are issued, before the activation
+// is quantized.
+template <int WT, int BPP, int RB, int NMAT, int KS, int D, typename Hook>
+__device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int wg, char* smem,
+                                         const Hook& hook) {
+  constexpr int RPP = 16 / BPP;   // rows per pass
+  constexpr int LPR = 4 * BPP;    // lanes per row
+  constexpr int RG = RB * RPP;    // rows per row group
+  constexpr int WR = NW / KS;     // waves per k-split
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int K = A.K, N = A.N;
+  const bool q80 = WT == TPT_TYPE_Q8_0;
+  const int nb = K / QK_K;  // super-blocks (256 weights) per row
+  const Lds L = lds_layout(smem, K, q80);
+  const int RPW = geo.rows_per_wg;
+  const int r0 = wg * RPW;
+  const int rp = lane / LPR, sb = (lane / 4) % BPP, q = lane & 3;
+
+  // this wave's row groups and passes
+  const int ngrp = RPW / RG;
+  const int wr = wid / KS, ks = wid % KS;
+  // row groups wr, wr + WR, ...: at any step the waves of a k-split read adjacent rows, so a
+  // workgroup streams one contiguous window of the matrix
+  const int ng = ngrp > wr ? (ngrp - wr + WR - 1) / WR : 0;
+  const int pa = ks * geo.P / KS, pb = (ks + 1) * geo.P / KS;
+  const int PP = pb - pa;
+  const int S = ng * PP;
+
+
+  // 2. weight steps in a ring of D register slots (slot d holds steps d, d + D, ...), the first
+  //    D issued before the prologue
+  Raw<WT> ring[D][RB][NMAT];
+  auto group_of = [&](int p, bool* valid) {  // this lane's weight group in pass p
+    const int blk = p * BPP + sb;
+    *valid = blk < nb;
+    return 4 * (blk < nb ? blk : nb - 1) + q;
+  };
+  auto issue = [&](Raw<WT> (&buf)[RB][NMAT], int s) {
+    if (s >= S) s = S > 0 ? S - 1 : 0;  // past the end: re-read the last step (cache hits)
+    const int pp = PP > 0 ? PP : 1;
+    const int grp = wr + (s / pp) * WR, p = pa + s % pp;
+    bool v;
+    const int g = group_of(p, &v);
+#pragma unroll
+    for (int j = 0; j < RB; j++) {
+      int row = r0 + (grp * RB + j) * RPP + rp;
+      if (row >= N) row = N - 1;
+#pragma unroll
+      for (int m = 0; m < NMAT; m++)
+        load_raw<WT>((m == 0 ? A.w0 : A.w1) + (size_t)row * A.row_stride, g, buf[j][m]);
+    }
+  };
+  // 1. activation values first: the loads complete in issue order, so the prologue below only
+  //    waits for these, not for the weights issued after them
+  XPre xp;
+  preload_x<WT != TPT_TYPE_Q8_0>(A, xp);
+#pragma unroll
+  for (int d = 0; d < D; d++) issue(ring[d], d);
+  hook();
+  if constexpr (WT == TPT_TYPE_Q8_0) prologue_q80(A, xp, L);
+  else prologue_q8k(A, xp, L);
+  barrier_lds();
+
+  float acc[RB][NMAT];
+#pragma unroll
+  for (int j = 0; j < RB; j++)
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) acc[j][m] = 0.f;
+
+  auto compute = [&](const Raw<WT> (&buf)[RB][NMAT], int s) {
+    const int grp = wr + (s / PP) * WR, p = pa + s % PP;
+    bool v;
+    const int g = group_of(p, &v);
+    Act act;
+    load_act<WT>(L, g, act);
+#pragma unroll
+    for (int j = 0; j < RB; j++)
+#pragma unroll
+      for (int m = 0; m < NMAT; m++) {
+        const float t = dot_group(buf[j][m], act, g);
+        acc[j][m] += v ? t : 0.f;
+      }
+    if (p == pb - 1) {  // row group done: row totals to LDS
+#pragma unroll
+      for (int j = 0; j < RB; j++)
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) {
+          const float t = lane_group_sum<LPR>(acc[j][m]);
+          if (lane % LPR == 0) L.rows[((size_t)ks * RPW + (grp * RB + j) * RPP + rp) * NMAT + m] = t;
+          acc[j][m] = 0.f;
+        }
+    }
+  };
+
+  if (S > 0) {
+    for (int s = 0; s < S; s += D) {
+#pragma unroll
+      for (int d = 0; d < D; d++) {
+        if (s + d < S) compute(ring[d], s + d);
+        issue(ring[d], s + d + D);  // unconditional: the slot's next step
+      }
+    }
+  }
+  __syncthreads();
+
+  // 3. epilogue over the workgroup's rows
+  const int nrows = min(RPW, N - r0);
+  int pos = 0;
+  if (A.epilogue == EPI_ROPE_QKV) pos = A.state ? A.state->pos : A.pos_host;
+  auto row_val = [&](int i, int m) {
+    float t = 0.f;
+#pragma unroll
+    for (int k = 0; k < KS; k++) t += L.rows[((size_t)k * RPW + i) * NMAT + m];
+    return t;
+  };
+  switch (A.epilogue) {
+    case EPI_STORE:
+      for (int i = tid; i < nrows; i += NT) A.y[r0 + i] = row_val(i, 0);
+      break;
+    case EPI_RESID:
+      for (int i = tid; i < nrows; i += NT) A.y[r0 + i] = row_val(i, 0) + A.resid[r0 + i];
+      break;
+    case EPI_SWIGLU:
+      for (int i = tid; i < nrows; i += NT) {
+        const float g = row_val(i, 0);
+        A.y[r0 + i] = silu_mul(g, row_val(i, NMAT - 1));
+      }
+      break;
+    case EPI_ARGMAX: {
+      unsigned long long best = 0;
+      for (int i = tid; i < nrows; i += NT) {
+        const float v = row_val(i, 0);
+        if (A.y) A.y[r0 + i] = v;
+        const unsigned long long key =
+            ((unsigned long long)order_key(v) << 32) | (unsigned long long)(r0 + i);
+        best = key > best ? key : best;
+      }
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const unsigned long long ob = __shfl_xor(best, o, WAVE);
+        best = ob > best ? ob : best;
+      }
+      // one atomic per workgroup: the waves' maxima meet in LDS (the row buffer is free now)
+      unsigned long long* wbest = (unsigned long long*)L.q32;
+      __syncthreads();
+      if (lane == 0) wbest[wid] = best;
+      __syncthreads();
+      if (tid == 0) {
+        unsigned long long b = 0;
+#pragma unroll
+        for (int w = 0; w < NW; w++) b = wbest[w] > b ? wbest[w] : b;
+        if (b) atomicMax(A.amax + (A.state ? A.state->parity : 0), b);
+      }
+    } break;
+    case EPI_ROPE_QKV:
+      // rows come in (even, odd) pairs; r0 and nrows are even
+      for (int i = 2 * tid; i < nrows; i += 2 * NT) {
+        const float x0 = row_val(i, 0), x1 = row_val(i + 1, 0);
+        const int lrow = A.row0 + r0 + i;
+        if (lrow < A.qd + A.kd) {
+          const bool isq = lrow < A.qd;
+          const int rr = isq ? lrow : lrow - A.qd;
+          const size_t ti = (size_t)pos * (A.hd / 2) + ((rr % A.hd) >> 1);
+          const float cs = A.rope_cos[ti], sn = A.rope_sin[ti];
+          // candle rope_i: dst[2i] = x0*cos - x1*sin; dst[2i+1] = x0*sin + x1*cos
+          const float o0 = x0 * cs - x1 * sn, o1 = x0 * sn + x1 * cs;
+          if (isq) {
+            A.y[rr] = o0;
+            A.y[rr + 1] = o1;
+          } else {
+            const size_t ci = ((size_t)(rr / A.hd) * A.max_ctx + pos) * A.hd + rr % A.hd;
+            store_kv_pair(A.kcache, A.kv_type, ci, o0, o1);
+          }
+        } else {
+          const int rr = lrow - A.qd - A.kd;
+          const size_t ci = ((size_t)(rr / A.hd) * A.max_ctx + pos) * A.hd + rr % A.hd;
+          store_kv_pair(A.vcache, A.kv_type, ci, x0, x1);
+        }
+      }
+      break;
+  }
+}
+}  // namespace gemv
+}  // namespace tpt

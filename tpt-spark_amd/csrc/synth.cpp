@@ -234,7 +234,6 @@ typedef struct {
   float rope_base, rms_eps, init_std;
   int type_matrix, type_embd, type_out;
   uint32_t eos_token_id;
-  float resid_std;  // std of attn_output / ffn_down (the residual-branch outputs); 0: init_std
 } tpt_synth_cfg;
 
 // Quantize n floats (a whole number of blocks) into GGUF blocks of `type`.
@@ -258,7 +257,6 @@ int tpt_synth_write_llama(const char* path, const tpt_synth_cfg* c, uint64_t see
   auto add = [&](const std::string& n, int t, int64_t ne0, int64_t ne1, int init) {
     ts.push_back({n, t, ne0, ne1, init, 0, 0});
   };
-  // init 0: N(0, init_std); 1: ones; 2: N(0, resid_std)
   add("token_embd.weight", c->type_embd, H, V, 0);
   add("output_norm.weight", T_F32, H, 1, 1);
   add("output.weight", c->type_out, H, V, 0);
@@ -268,11 +266,11 @@ int tpt_synth_write_llama(const char* path, const tpt_synth_cfg* c, uint64_t see
     add(p + "attn_q.weight", c->type_matrix, H, qd, 0);
     add(p + "attn_k.weight", c->type_matrix, H, kd, 0);
     add(p + "attn_v.weight", c->type_matrix, H, kd, 0);
-    add(p + "attn_output.weight", c->type_matrix, qd, H, 2);
+    add(p + "attn_output.weight", c->type_matrix, qd, H, 0);
     add(p + "ffn_norm.weight", T_F32, H, 1, 1);
     add(p + "ffn_gate.weight", c->type_matrix, H, F, 0);
     add(p + "ffn_up.weight", c->type_matrix, H, F, 0);
-    add(p + "ffn_down.weight", c->type_matrix, F, H, 2);
+    add(p + "ffn_down.weight", c->type_matrix, F, H, 0);
   }
   const uint64_t ALIGN = 32;
   uint64_t off = 0;
@@ -337,11 +335,10 @@ int tpt_synth_write_llama(const char* path, const tpt_synth_cfg* c, uint64_t see
     // 256 elements per work unit for every type (Q8_0: 8 blocks)
     const int per = 256 / be;
     const int64_t units = nblk / per;
-    const float std = t.init == 2 && c->resid_std > 0.f ? c->resid_std : c->init_std;
     auto work = [&](int tid) {
       float buf[256];
       for (int64_t u = (int64_t)tid * units / nthreads; u < (int64_t)(tid + 1) * units / nthreads; u++) {
-        normals(key, u * 256, 256, std, buf);
+        normals(key, u * 256, 256, c->init_std, buf);
         quantize(t.type, buf, 256, dst + (size_t)u * per * bb);
       }
     };

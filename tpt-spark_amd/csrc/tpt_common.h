@@ -164,6 +164,49 @@ __device__ __forceinline__ uint32_t order_key(float f) {
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+// One element of a GGUF row, dequantized with candle's to_float arithmetic (bit-exact):
+//   Q4_K: (d*sc)*q - dmin*m     (candle BlockQ4K::to_float; ggml dequantize_row_q4_K order)
+//   Q6_K: (d*sc)*(q-32)         (candle BlockQ6K::to_float; dequant_q6k.wgsl:9-24 layout)
+//   Q8_0: d*q                   (candle BlockQ8_0::to_float; dequant_q8.wgsl:3-6)
+__device__ __forceinline__ float dequant_elem(int type, const uint8_t* base, int64_t i) {
+  if (type == TPT_TYPE_Q4_K) {
+    const uint8_t* b = base + (i >> 8) * 144;
+    const int j = (int)(i & 255), g = j >> 6, l = j & 63;
+    const int sub = 2 * g + (l >= 32);
+    const uint8_t qb = b[16 + 32 * g + (l & 31)];
+    const int q = l < 32 ? (qb & 0xF) : (qb >> 4);
+    const uint8_t* s = b + 4;
+    int sc, m;
+    if (sub < 4) {
+      sc = s[sub] & 63;
+      m = s[sub + 4] & 63;
+    } else {
+      sc = (s[sub + 4] & 0xF) | ((s[sub - 4] >> 6) << 4);
+      m = (s[sub + 4] >> 4) | ((s[sub] >> 6) << 4);
+    }
+    const float d = h2f(ldg_u<uint16_t>(b)), dmin = h2f(ldg_u<uint16_t>(b + 2));
+    const float d1 = d * (float)sc, m1 = dmin * (float)m;
+    return d1 * (float)q - m1;
+  }
+  if (type == TPT_TYPE_Q6_K) {
+    const uint8_t* b = base + (i >> 8) * 210;
+    const int j = (int)(i & 255), p = j >> 7, r = j & 127, quad = r >> 5, l = r & 31;
+    const uint8_t qlb = b[64 * p + 32 * (quad & 1) + l];
+    const int lo = quad >= 2 ? (qlb >> 4) : (qlb & 0xF);
+    const int hi = (b[128 + 32 * p + l] >> (2 * quad)) & 3;
+    const int q = (lo | (hi << 4)) - 32;
+    const int sc = (int8_t)b[192 + 8 * p + (l >> 4) + 2 * quad];
+    const float d = h2f(ldg_u<uint16_t>(b + 208));
+    return d * (float)sc * (float)q;
+  }
+  if (type == TPT_TYPE_Q8_0) {
+    const uint8_t* b = base + (i >> 5) * 34;
+    return h2f(ldg_u<uint16_t>(b)) * (float)(int8_t)b[2 + (i & 31)];
+  }
+  if (type == TPT_TYPE_F16) return h2f(ldg_u<uint16_t>(base + 2 * i));
+  return ldg_u<float>(base + 4 * i);
+}
+
 // ---------------------------------------------------------------- errors
 
 void set_error(const std::string& msg);

@@ -17,7 +17,7 @@ class SynthCfg(C.Structure):
                                        "context_length")] + \
                [("rope_base", C.c_float), ("rms_eps", C.c_float), ("init_std", C.c_float)] + \
                [(n, C.c_int) for n in ("type_matrix", "type_embd", "type_out")] + \
-               [("eos_token_id", C.c_uint32), ("resid_std", C.c_float)]
+               [("eos_token_id", C.c_uint32)]
 
 
 def lib():
@@ -44,13 +44,10 @@ TINY = dict(n_layers=2, embed=256, n_heads=4, n_kv_heads=2, ffn=512, vocab=1024,
 
 
 def write_llama(path, cfg, seed=0, nthreads=0, init_std=0.02, type_matrix=TYPE_Q4_K,
-                type_embd=TYPE_Q6_K, type_out=TYPE_Q6_K, resid_std=0.0):
-    """All matrices N(0, init_std) except attn_output / ffn_down, which take resid_std when it
-    is > 0 (the scaled residual init, init_std / sqrt(2 * n_layers), keeps a deep random model
-    from amplifying rounding differences the way a trained one does not)."""
+                type_embd=TYPE_Q6_K, type_out=TYPE_Q6_K):
     c = SynthCfg(cfg["n_layers"], cfg["embed"], cfg["n_heads"], cfg["n_kv_heads"], cfg["ffn"],
                  cfg["vocab"], cfg["context_length"], cfg["rope_base"], cfg["rms_eps"], init_std,
-                 type_matrix, type_embd, type_out, cfg.get("eos_token_id", 0), resid_std)
+                 type_matrix, type_embd, type_out, cfg.get("eos_token_id", 0))
     rc = lib().tpt_synth_write_llama(path.encode(), C.byref(c), seed, nthreads)
     if rc:
         raise RuntimeError(f"tpt_synth_write_llama({path}) failed: {rc}")
