@@ -57,7 +57,8 @@ __global__ void __launch_bounds__(ANT) attn_partial_kernel(const AttnArgs a, con
   const int plast = min(p0 + CL, a.L_stride) - 1;  // clamped loads stay inside the cache
   const int L = (a.state ? a.state->pos + 1 : a.L_host) + t;
   const int p1 = min(L, p0 + CL);
-  const int n = p1 - p0;  // may be <= 0 for trailing chunks
+  const int n = p1 - p0;
+  if (n <= 0) return;  // a chunk past the live length: the merge does not read its record
 
   const T* K = (const T*)a.kc + (size_t)kvh * a.L_stride * HD + li * EPL;
   const T* V = (const T*)a.vc + (size_t)kvh * a.L_stride * HD + li * EPL;
@@ -195,7 +196,8 @@ __global__ void __launch_bounds__(ANT) attn_partial_kernel(const AttnArgs a, con
 // 32 consecutive output dims of one head; thread (set, j) sums chunks set, set + 8, ...
 template <int HD, int G>
 __global__ void __launch_bounds__(ANT) attn_merge_kernel(const float* __restrict__ part,
-                                                         float* __restrict__ out, int nch, int ldo) {
+                                                         float* __restrict__ out, int nch, int ldo,
+                                                         const StepState* state, int L_host, int CL) {
   constexpr int PSTRIDE = HD + 2;
   constexpr int TILES = G * HD / MT;  // merge workgroups per kv head
   __shared__ float s_w[NCH_MAX];
@@ -213,6 +215,9 @@ __global__ void __launch_bounds__(ANT) attn_merge_kernel(const float* __restrict
   float v0[8];
 #pragma unroll
   for (int i = 0; i < 8; i++) v0[i] = src[(size_t)min(set + i * MSETS, nch - 1) * G * PSTRIDE];
+  // chunks that hold positions of this query (the others wrote no record)
+  const int L = (state ? state->pos + 1 : L_host) + t;
+  nch = min(nch, (L + CL - 1) / CL);
   if (tid < WAVE) {
     float mm = -INFINITY;
     for (int c = lane; c < nch; c += WAVE) mm = fmaxf(mm, pk[(size_t)c * G * PSTRIDE + HD]);
@@ -263,7 +268,8 @@ int launch_g(const AttnArgs& a, float scale, hipStream_t s) {
     hipLaunchKernelGGL((attn_partial_kernel<T, HD, G, 8>), grid, dim3(ANT), 0, s, a, scale);
   TPT_HIP(hipGetLastError());
   hipLaunchKernelGGL((attn_merge_kernel<HD, G>), dim3((unsigned)(a.nkv * G * HD / MT), (unsigned)a.nqb),
-                     dim3(ANT), 0, s, (const float*)a.part, a.o, a.n_chunks, a.ldo);
+                     dim3(ANT), 0, s, (const float*)a.part, a.o, a.n_chunks, a.ldo, a.state, a.L_host,
+                     a.chunk_len);
   TPT_HIP(hipGetLastError());
   return TPT_OK;
 }

@@ -246,7 +246,8 @@ int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_t
   desc.kv_type = kv_type;
   kv_elem = kv_type == TPT_TYPE_F32 ? 4 : 2;
   attn_max_chunks = attn_default_chunks(max_ctx, nkv);
-  for (int b = 64; b < max_ctx * 2; b *= 2) attn_max_chunks = std::max(attn_max_chunks, attn_default_chunks(b, nkv));
+  for (int L = 1; L <= max_ctx; L = bucket_of(L) + 1)
+    attn_max_chunks = std::max(attn_max_chunks, attn_default_chunks(bucket_of(L), nkv));
   const size_t kv_elems = (size_t)desc.n_layers * 2 * nkv * (size_t)max_ctx * hd;
   size_t ro = 0;
   auto carve = [&](size_t bytes) { size_t o = ro; ro = align_up(ro + bytes, 256); return o; };
@@ -301,9 +302,11 @@ int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_t
   return TPT_OK;
 }
 
-// Attention partition of the length bucket holding L (powers of two from 64): the chunk count
-// and chunk length are fixed per bucket, so one captured graph serves every length in it.
+// Attention partition of the length bucket holding L (64, 128, 256, 512, then multiples of
+// 512): the chunk count and chunk length are fixed per bucket, so one captured graph serves every
+// length in it, and chunks past the live length cost an early exit only.
 int tpt_model::bucket_of(int L) const {
+  if (L > 512) return (L + 511) / 512 * 512;
   int b = 64;
   while (b < L) b *= 2;
   return b;
