@@ -186,6 +186,19 @@ int tpt_model_decode_greedy(tpt_model* m, uint32_t first, int pos0, int n_steps,
                             int64_t stop_token, uint32_t* tokens_out);
 /* Copy the current residual stream (fp32 [embed]) to host memory (parity tests). */
 int tpt_model_hidden(tpt_model* m, float* out_host);
+/* How a decode step runs on the device.  Replaces the per-token loop of
+ * WgpuEngine::run_forward_pass (src-tauri/src/engine/wgpu_engine.rs:339-490), which submits
+ * each op of each layer separately.  TPT_DECODE_KERNELS: one launch per fused op (6 per
+ * layer), captured into a HIP graph per step.  TPT_DECODE_PERSISTENT: the embedding and every
+ * layer in one launch of one workgroup per compute unit, with grid barriers between the
+ * phases, then the LM head launch; available where the model's shape has such a kernel (every
+ * layer matrix Q4_K; TPT_ERR_UNSUPPORTED otherwise).  The default is TPT_DECODE_KERNELS (the
+ * environment variable TPT_HIP_DECODE=persistent selects the other at load).  Both paths run
+ * the same arithmetic in the same order: their logits and tokens are bit-identical. */
+#define TPT_DECODE_KERNELS 0
+#define TPT_DECODE_PERSISTENT 1
+int tpt_model_set_decode_path(tpt_model* m, int path);
+int tpt_model_get_decode_path(const tpt_model* m, int* path);
 /* Layer-range forward for parity checks (no counterpart in the reference): runs decoder layers
  * [l0, l1) on n caller-given residual rows x_in (host fp32 [n][embed]) at positions
  * pos0 .. pos0+n-1 and writes the resulting rows to x_out (host, same shape).  The layers' K/V

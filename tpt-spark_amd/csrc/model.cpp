@@ -50,6 +50,7 @@ tpt_model::~tpt_model() {
   if (arena) (void)hipFree(arena);
   if (runtime) (void)hipFree(runtime);
   if (pf_mem) (void)hipFree(pf_mem);
+  if (dec_mem) (void)hipFree(dec_mem);
   if (st_host) (void)hipHostFree(st_host);
   if (ids_host) (void)hipHostFree(ids_host);
 }
@@ -298,7 +299,106 @@ int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_t
   if (ev_pf && strcmp(ev_pf, "steps") == 0) batched_prefill = false;
   const char* ev_graph = getenv("TPT_HIP_GRAPHS");
   use_graphs = !(ev_graph && ev_graph[0] == '0');
+  if ((rc = setup_decode_layers())) return rc;
   TPT_HIP(hipStreamSynchronize(stream));
+  return TPT_OK;
+}
+
+// The persistent decode step needs every layer matrix in Q4_K with q|k|v adjacent, q width =
+// embedding width, and a compiled instantiation whose LDS fits every length bucket's attention
+// partition.  It is selected with TPT_HIP_DECODE=persistent or tpt_model_set_decode_path.
+int tpt_model::setup_decode_layers() {
+  decode_layers_ok = use_decode_layers = false;
+  const int H = desc.embed, hd = desc.head_dim, nq = desc.n_heads, nkv = desc.n_kv_heads;
+  const int qd = nq * hd, kd = nkv * hd, mc = desc.max_ctx;
+  for (const Layer& L : layers) {
+    if (!L.qkv_adjacent) return TPT_OK;
+    for (int t : {L.tq, L.to, L.tg, L.tu, L.td})
+      if (t != TPT_TYPE_Q4_K) return TPT_OK;
+  }
+  DecodeArgs d;
+  d.n_layers = desc.n_layers;
+  d.H = H; d.qd = qd; d.kd = kd; d.hd = hd; d.nq = nq; d.nkv = nkv; d.F = desc.ffn;
+  d.max_ctx = mc; d.vocab = desc.vocab;
+  d.eps = desc.rms_eps;
+  d.attn_scale = (float)(1.0 / sqrt((double)hd));  // the scale launch_attn_decode uses
+  d.embd = embd; d.embd_type = embd_type; d.embd_row = embd_row;
+  d.kv = kv; d.kv_type = desc.kv_type; d.layer_kv_bytes = (size_t)2 * nkv * mc * hd * kv_elem;
+  d.x = x; d.q = qbuf; d.att = attn; d.h = hbuf; d.part = attn_part;
+  d.rope_cos = rope_cos; d.rope_sin = rope_sin;
+  d.st = st; d.prompt = prompt_dev; d.tok_log = tok_log;
+  d.s_h = row_bytes(TPT_TYPE_Q4_K, H); d.s_q = row_bytes(TPT_TYPE_Q4_K, qd);
+  d.s_f = row_bytes(TPT_TYPE_Q4_K, desc.ffn);
+  for (int L = 1; L <= mc; L = bucket_of(L) + 1) {  // every bucket's partition must fit
+    DecodeArgs t = d;
+    const int b = bucket_of(L);
+    t.n_chunks = std::min(attn_default_chunks(b, nkv), attn_max_chunks);
+    t.chunk_len = attn_chunk_len(b, t.n_chunks);
+    if (decode_layers_plan(ctx, t) != TPT_OK) {
+      set_error("");  // not an error: this model decodes with one launch per op
+      return TPT_OK;
+    }
+    if (L == 1) d.grid = t.grid;
+  }
+  // barrier state (flags, epoch, error word: one 128-byte line each), then the layer table
+  const size_t line = 128;
+  dec_sync_bytes = line * ((size_t)d.grid + 2);
+  const size_t tab = sizeof(DecLayer) * desc.n_layers;
+  TPT_HIP(hipMalloc(&dec_mem, dec_sync_bytes + tab));
+  uint8_t* m = (uint8_t*)dec_mem;
+  d.flags = (unsigned*)m;
+  d.epoch = (unsigned*)(m + line * d.grid);
+  d.err = (unsigned*)(m + line * (d.grid + 1));
+  d.layers = (const DecLayer*)(m + dec_sync_bytes);
+  std::vector<DecLayer> t(desc.n_layers);
+  for (int l = 0; l < desc.n_layers; l++) {
+    const Layer& L = layers[l];
+    t[l].qkv = L.q; t[l].o = L.o; t[l].gate = L.gate; t[l].up = L.up; t[l].down = L.down;
+    t[l].attn_norm = L.attn_norm; t[l].ffn_norm = L.ffn_norm;
+  }
+  TPT_HIP(hipMemcpy(m + dec_sync_bytes, t.data(), tab, hipMemcpyHostToDevice));
+  dec = d;
+  int rc = dec_reset();
+  if (rc) return rc;
+  decode_layers_ok = true;
+  // measured on the 8B shape at 2K positions: 1.93 ms/token with one launch per op, 2.09 ms with
+  // the persistent kernel, so the per-op launches stay the default
+  const char* ev = getenv("TPT_HIP_DECODE");
+  use_decode_layers = ev && strcmp(ev, "persistent") == 0;
+  return TPT_OK;
+}
+
+int tpt_model::dec_reset() {
+  TPT_HIP(hipStreamSynchronize(stream));
+  TPT_HIP(hipMemsetAsync(dec_mem, 0, dec_sync_bytes, stream));  // outside any graph
+  TPT_HIP(hipStreamSynchronize(stream));
+  dec_epochs = 0;
+  return TPT_OK;
+}
+
+int tpt_model::dec_check() {
+  if (!decode_layers_ok) return TPT_OK;
+  unsigned err = 0;
+  TPT_HIP(hipMemcpyAsync(&err, dec.err, 4, hipMemcpyDeviceToHost, stream));
+  TPT_HIP(hipStreamSynchronize(stream));
+  if (!err) return TPT_OK;
+  int rc = dec_reset();
+  if (rc) return rc;
+  return fail(TPT_ERR_HIP, "decode step: a grid barrier wait timed out (not every workgroup of the persistent kernel was resident); results of this call are invalid");
+}
+
+int tpt_model::set_decode_path(int path) {
+  if (path != TPT_DECODE_KERNELS && path != TPT_DECODE_PERSISTENT)
+    return fail(TPT_ERR_INVALID, "decode path must be TPT_DECODE_KERNELS or TPT_DECODE_PERSISTENT");
+  if (path == TPT_DECODE_PERSISTENT && !decode_layers_ok)
+    return fail(TPT_ERR_UNSUPPORTED, "no persistent decode kernel for this model's shape or types");
+  const bool want = path == TPT_DECODE_PERSISTENT;
+  if (want != use_decode_layers) {
+    TPT_HIP(hipStreamSynchronize(stream));
+    for (auto& kv : graphs) (void)hipGraphExecDestroy(kv.second);
+    graphs.clear();
+    use_decode_layers = want;
+  }
   return TPT_OK;
 }
 
@@ -315,11 +415,19 @@ int tpt_model::bucket_of(int L) const {
 int tpt_model::enqueue_step(int bucket, bool lm_head) {
   const int n_chunks = std::min(attn_default_chunks(bucket, desc.n_kv_heads), attn_max_chunks);
   const int chunk_len = attn_chunk_len(bucket, n_chunks);
-  int rc = launch_step_begin(st, prompt_dev, embd_type, embd, embd_row, desc.embed, desc.vocab, x,
-                             tok_log, stream);
-  if (rc) return rc;
-  for (int l = 0; l < desc.n_layers; l++)
-    if ((rc = enqueue_layer(l, n_chunks, chunk_len))) return rc;
+  int rc;
+  if (use_decode_layers) {
+    DecodeArgs d = dec;
+    d.n_chunks = n_chunks;
+    d.chunk_len = chunk_len;
+    if ((rc = decode_layers_plan(ctx, d)) || (rc = launch_decode_layers(d, stream))) return rc;
+  } else {
+    if ((rc = launch_step_begin(st, prompt_dev, embd_type, embd, embd_row, desc.embed, desc.vocab,
+                                x, tok_log, stream)))
+      return rc;
+    for (int l = 0; l < desc.n_layers; l++)
+      if ((rc = enqueue_layer(l, n_chunks, chunk_len))) return rc;
+  }
   if (lm_head) {
     GemvArgs lh;
     lh.w0 = out;
@@ -442,6 +550,14 @@ int tpt_model::enqueue_layer(int l, int n_chunks, int chunk_len) {
 
 int tpt_model::launch_step(int L, bool lm_head) {
   if (L > desc.max_ctx) return fail(TPT_ERR_STATE, "context length exhausted");
+  if (use_decode_layers) {  // barrier epochs are 32-bit: clear the state long before they wrap
+    const uint64_t nb = (uint64_t)decode_layers_barriers(desc.n_layers);
+    if (dec_epochs + nb > 0xF0000000ull) {
+      int rc = dec_reset();
+      if (rc) return rc;
+    }
+    dec_epochs += nb;
+  }
   const int nch = bucket_of(L);
   if (!use_graphs || !lm_head) return enqueue_step(nch, lm_head);
   auto it = graphs.find(nch);
@@ -675,7 +791,7 @@ int tpt_model::prefill(const uint32_t* ids, int n, int pos0, uint32_t* next_out,
     return rc;
   }
   StepState s;
-  if ((rc = read_state(&s))) return rc;
+  if ((rc = read_state(&s)) || (rc = dec_check())) return rc;
   if (next_out) *next_out = (uint32_t)(s.amax[s.parity] & 0xffffffffull);
   if (logits_out) {
     TPT_HIP(hipMemcpyAsync(logits_out, logits, (size_t)desc.vocab * 4, hipMemcpyDeviceToHost, stream));
@@ -728,6 +844,7 @@ int tpt_model::decode_stream(uint32_t first, int pos0, int n_steps, StepFn fn, v
   for (hipEvent_t ev : evs) (void)hipEventDestroy(ev);
   if (rc) return rc;
   if (e != hipSuccess) return hip_fail(e, "decode", __FILE__, __LINE__);
+  if ((rc = dec_check())) return rc;
   if (!stop && (rc = deliver(launched - 1))) return rc;
   if (!stop && delivered == launched - 1) {
     StepState s;
@@ -833,6 +950,19 @@ int tpt_model_kv_read(tpt_model* m, int layer, void* k_host, void* v_host) {
   TPT_HIP(hipMemcpyAsync(k_host, kc, half, hipMemcpyDeviceToHost, m->stream));
   TPT_HIP(hipMemcpyAsync(v_host, kc + half, half, hipMemcpyDeviceToHost, m->stream));
   TPT_HIP(hipStreamSynchronize(m->stream));
+  return TPT_OK;
+}
+
+int tpt_model_set_decode_path(tpt_model* m, int path) {
+  if (!m) return fail(TPT_ERR_INVALID, "null argument");
+  int rc = ctx_enter(m->ctx);
+  if (rc) return rc;
+  return m->set_decode_path(path);
+}
+
+int tpt_model_get_decode_path(const tpt_model* m, int* path) {
+  if (!m || !path) return fail(TPT_ERR_INVALID, "null argument");
+  *path = m->use_decode_layers ? TPT_DECODE_PERSISTENT : TPT_DECODE_KERNELS;
   return TPT_OK;
 }
 

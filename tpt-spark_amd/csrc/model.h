@@ -49,6 +49,18 @@ struct tpt_model {
   bool use_graphs = true;
   std::map<int, hipGraphExec_t> graphs;  // by length bucket
 
+  // persistent decode step (k_decode.hip): embedding + all layers in one launch
+  bool decode_layers_ok = false;   // a persistent kernel exists for this shape
+  bool use_decode_layers = false;  // decode steps run it (else one launch per op)
+  tpt::DecodeArgs dec{};           // its arguments except the attention partition
+  void* dec_mem = nullptr;         // layer table + barrier flags, epoch, counters, error word
+  size_t dec_sync_bytes = 0;       // bytes of the barrier state at the start of dec_mem
+  uint64_t dec_epochs = 0;         // barrier epochs issued since the state was last cleared
+  int setup_decode_layers();
+  int set_decode_path(int path);
+  int dec_reset();                 // clears the barrier state (synchronizes the stream)
+  int dec_check();                 // reports a timed-out barrier wait, then clears the state
+
   // batched prefill (MFMA GEMMs over up to kPrefillT positions at once)
   static constexpr int kPrefillT = 1024;
   bool batched_prefill = false;       // every layer matrix is Q4_K

@@ -88,6 +88,8 @@ EXPORTS = {
     "tpt_model_hidden": ([P, P], I32),
     "tpt_model_run_layers": ([P, P, I32, I32, I32, I32, I32, P], I32),
     "tpt_model_kv_read": ([P, I32, P, P], I32),
+    "tpt_model_set_decode_path": ([P, I32], I32),
+    "tpt_model_get_decode_path": ([P, P], I32),
     "tpt_engine_create": ([I32, P], I32),
     "tpt_engine_set_kv_type": ([P, I32], I32),
     "tpt_engine_destroy": ([P], I32),
@@ -355,6 +357,19 @@ class Model:
         return out
 
     PATH_BATCHED, PATH_STEPS = 0, 1
+    DECODE_KERNELS, DECODE_PERSISTENT = 0, 1
+
+    @property
+    def decode_path(self):
+        """DECODE_PERSISTENT: embedding + all layers of a decode step in one launch (grid
+        barriers between phases); DECODE_KERNELS: one launch per fused op."""
+        v = C.c_int()
+        check(lib().tpt_model_get_decode_path(self.h, C.byref(v)))
+        return v.value
+
+    @decode_path.setter
+    def decode_path(self, path):
+        check(lib().tpt_model_set_decode_path(self.h, path))
 
     def kv(self, layer):
         """Layer's K and V caches as float32 arrays [n_kv_heads, max_ctx, head_dim]."""
