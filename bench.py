@@ -81,6 +81,38 @@ def gemv_roofline(tp, ctx, iters=256):
     return out
 
 
+# decode attention at the long-context shapes: GQA 32/8 hd 128 and MHA 32/32 hd 96, fp16 cache
+ATTN_CASES = [(32, 8, 128, 512), (32, 8, 128, 4096), (32, 8, 128, 16384), (32, 8, 128, 32768),
+              (32, 32, 96, 4096), (32, 32, 96, 16384)]
+
+
+def attn_roofline(tp, ctx, iters=64):
+    """Event-timed split-K decode attention (partial + merge launches) at ATTN_CASES, rotating
+    through >= 1.1 GB of distinct K/V caches.  Algorithmic bytes per call = K and V rows read
+    once (2 * Nkv * L * hd * 2 B) + q and o (2 * Nq * hd * 4 B)."""
+    out = {}
+    rng = np.random.default_rng(7)
+    for nq, nkv, hd, L in ATTN_CASES:
+        k = rng.standard_normal((nkv, L, hd), dtype=np.float32).astype(np.float16)
+        n_copies = max(2, int(np.ceil(1.1e9 / (2 * k.nbytes))))
+        ks = [ctx.to_device(k) for _ in range(n_copies)]
+        vs = [ctx.to_device(k) for _ in range(n_copies)]
+        q = ctx.to_device(rng.standard_normal(nq * hd, dtype=np.float32))
+        o = ctx.alloc(nq * hd * 4)
+        ctx.bench_attn(q, ks, vs, o, nq, nkv, hd, L, L, n_copies)  # warm-up pass
+        n = max(iters, n_copies)
+        ms = ctx.bench_attn(q, ks, vs, o, nq, nkv, hd, L, L, n)
+        alg = 2 * nkv * L * hd * 2 + 2 * nq * hd * 4
+        us = ms * 1e3 / n
+        gbs = alg / (us * 1e-6) / 1e9
+        out[f"{nq}/{nkv}x{hd}@{L}"] = {"bytes": alg, "us_per_call": round(us, 3), "gbs": round(gbs, 1),
+                                        "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": n_copies}
+        log(f"attention {nq}/{nkv} hd {hd} L {L}: {us:.2f} us/call, {gbs:.0f} GB/s")
+        for b in ks + vs + [q, o]:
+            b.free()
+    return out
+
+
 def cpu_baseline(path, budget_s=20.0):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
@@ -129,8 +161,9 @@ def main():
     ap.add_argument("--prompt", type=int, default=PROMPT_LEN)
     ap.add_argument("--model", default="", help="existing GGUF (default: generate the 8B shape)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--leg", choices=["all", "gemv"], default="all",
-                    help="gemv: only the GEMV roofline leg and the copy calibration (profiling)")
+    ap.add_argument("--leg", choices=["all", "gemv", "attn"], default="all",
+                    help="gemv: only the GEMV roofline leg and the copy calibration (profiling); "
+                         "attn: only the decode-attention leg")
     ap.add_argument("--gemv-iters", type=int, default=256, help="timed launches per GEMV shape")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -144,10 +177,14 @@ def main():
 
     ctx = tp.Context(0)
     log(f"device: {ctx.name}, {ctx.n_cu} CUs")
+    if args.leg == "attn":
+        print(json.dumps({"attn_decode": attn_roofline(tp, ctx)}))
+        return
     gemv = gemv_roofline(tp, ctx, iters=args.gemv_iters)
     if args.leg == "gemv":
         print(json.dumps({"gemv": gemv, "copy": copy_calibration(ctx)}))
         return
+    attn = attn_roofline(tp, ctx)
 
     tmpdir = tempfile.mkdtemp(prefix="tpt_bench_", dir=os.environ.get("TPT_BENCH_DIR") or None)
     path = args.model
@@ -224,6 +261,7 @@ def main():
             "decode_frac_of_ceiling_with_kv": round(tok_s / (HBM_PEAK_GBS * 1e9 / (bpt + kv_bpt)), 4),
             "arith": "q4_k/q6_k weights x q8_k activations: int8 dot4 -> int32, f32 block scales",
             "gemv_q4k": gemv,
+            "attn_decode_f16": attn,
         },
         "roofline": {
             "bound": "hbm",

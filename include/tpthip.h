@@ -133,10 +133,12 @@ int tpt_bench_gemv(tpt_ctx* ctx, int type, const void* const* weights, int n_wei
  * timed launches); *ms_out = the sum of the dispatch-stamped event intervals. */
 int tpt_bench_gemm(tpt_ctx* ctx, int type, const void* w, const float* x, float* y, int M, int K,
                    int N, int act_mode, int iters, float* ms_out);
-/* iters launches of tpt_attn_decode over the same cache; *ms_out = total event time */
-int tpt_bench_attn(tpt_ctx* ctx, const float* q, const void* k_cache, const void* v_cache,
-                   int kv_type, float* o, int nq, int nkv, int hd, int L, int L_stride,
-                   int n_chunks, int iters, float* ms_out);
+/* iters back-to-back launches of tpt_attn_decode, launch i reading the caches
+ * k_caches[i % n_caches] / v_caches[i % n_caches] (distinct copies defeat the Infinity Cache);
+ * *ms_out = the event time over all launches (events recorded on the context's stream). */
+int tpt_bench_attn(tpt_ctx* ctx, const float* q, const void* const* k_caches,
+                   const void* const* v_caches, int n_caches, int kv_type, float* o, int nq,
+                   int nkv, int hd, int L, int L_stride, int n_chunks, int iters, float* ms_out);
 /* iters launches of a plain vector copy of `bytes` (HBM calibration for PMC counters) */
 int tpt_bench_copy(tpt_ctx* ctx, void* dst, const void* src, size_t bytes, int iters,
                    float* ms_out);

@@ -229,19 +229,26 @@ int tpt_attn_decode(tpt_ctx* c, const float* q, const void* k_cache, const void*
   return rc;
 }
 
-int tpt_bench_attn(tpt_ctx* c, const float* q, const void* k_cache, const void* v_cache,
-                   int kv_type, float* o, int nq, int nkv, int hd, int L, int L_stride,
-                   int n_chunks, int iters, float* ms_out) {
+int tpt_bench_attn(tpt_ctx* c, const float* q, const void* const* k_caches,
+                   const void* const* v_caches, int n_caches, int kv_type, float* o, int nq,
+                   int nkv, int hd, int L, int L_stride, int n_chunks, int iters, float* ms_out) {
   ENTER(c);
-  if (iters <= 0 || !ms_out) return fail(TPT_ERR_INVALID, "bench_attn: bad arguments");
+  if (iters <= 0 || iters > 4096 || !ms_out || !k_caches || !v_caches || n_caches <= 0)
+    return fail(TPT_ERR_INVALID, "bench_attn: bad arguments");
+  for (int i = 0; i < n_caches; i++)
+    if (!k_caches[i] || !v_caches[i]) return fail(TPT_ERR_INVALID, "bench_attn: null cache pointer");
   AttnCall call;
-  int rc = attn_prepare(c, q, k_cache, v_cache, kv_type, o, nq, nkv, hd, L, L_stride, n_chunks, &call);
+  int rc = attn_prepare(c, q, k_caches[0], v_caches[0], kv_type, o, nq, nkv, hd, L, L_stride, n_chunks, &call);
   if (rc) return rc;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   hipError_t e = hipEventCreate(&e0);
   if (e == hipSuccess) e = hipEventCreate(&e1);
   if (e == hipSuccess) e = hipEventRecord(e0, c->stream);
-  for (int i = 0; i < iters && rc == TPT_OK && e == hipSuccess; i++) rc = launch_attn_decode(call.a, c->stream);
+  for (int i = 0; i < iters && rc == TPT_OK && e == hipSuccess; i++) {
+    call.a.kc = k_caches[i % n_caches];
+    call.a.vc = v_caches[i % n_caches];
+    rc = launch_attn_decode(call.a, c->stream);
+  }
   if (e == hipSuccess) e = hipEventRecord(e1, c->stream);
   if (e == hipSuccess) e = hipEventSynchronize(e1);
   if (e == hipSuccess && rc == TPT_OK) e = hipEventElapsedTime(ms_out, e0, e1);

@@ -94,8 +94,9 @@ __device__ __forceinline__ void barrier_lds() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Activation preload.  Loads are unconditional (clamped block index, x itself as a dummy norm
-// source) so the waitcnt pass can count exactly how many later loads may stay in flight.
+// Activation preload.  Loads are unconditional (clamped block index) so the waitcnt pass can
+// count exactly how many later loads may stay in flight; the norm weights are loaded only for
+// an RMSNorm prologue (NORM).
 //  * Q8_K activations (Q4_K / Q6_K weights), ROWS16: one 256-block per 16-lane DPP row -- lane l
 //    of wave w holds elements 16(l%16) .. +15 of block 4(w + qi NW) + l/16, qi < MAXQ.
 //  * Q8_0 activations: one float4 per lane per 256-element block, blocks w, w + NW, ...
@@ -105,12 +106,12 @@ struct XPre {
   float4 w[MAXB];
 };
 
-template <bool ROWS16>
+template <bool ROWS16, bool NORM>
 __device__ __forceinline__ void preload_x(const GemvArgs& A, XPre& p) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int nb = A.K / 256;
   const float4* xs = (const float4*)A.x;
-  const float4* ws = (const float4*)(A.prologue == PRO_RMSNORM ? A.norm_w : A.x);
+  const float4* ws = (const float4*)A.norm_w;
   if constexpr (ROWS16) {
     const int k = lane >> 4, m = lane & 15;
 #pragma unroll
@@ -120,7 +121,7 @@ __device__ __forceinline__ void preload_x(const GemvArgs& A, XPre& p) {
 #pragma unroll
       for (int j = 0; j < 4; j++) {
         p.x[qi * 4 + j] = xs[b * 64 + m * 4 + j];
-        p.w[qi * 4 + j] = ws[b * 64 + m * 4 + j];
+        if constexpr (NORM) p.w[qi * 4 + j] = ws[b * 64 + m * 4 + j];
       }
     }
   } else {
@@ -129,7 +130,7 @@ __device__ __forceinline__ void preload_x(const GemvArgs& A, XPre& p) {
       int b = wid + i * NW;
       if (b >= nb) b = nb - 1;
       p.x[i] = xs[b * 64 + lane];
-      p.w[i] = ws[b * 64 + lane];
+      if constexpr (NORM) p.w[i] = ws[b * 64 + lane];
     }
   }
 }
@@ -191,12 +192,14 @@ __device__ __forceinline__ float4 apply_norm(float4 v, float4 w, float m, float 
 // (element order: lane, then element) comes from the ballot of the lanes that hold it;
 // iscale = -128/max, q = round-half-away(iscale * x) (the lower clamp never binds), d = 1/iscale.
 // A lane's 16 values are exactly one per-16 group, so its q sum is that group's bsum.
+// NM: 1 RMSNorm, 0 none, -1 as A.prologue says.
+template <int NM = -1>
 __device__ __forceinline__ void prologue_q8k(const GemvArgs& A, const XPre& p, const Lds& L) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int k = lane >> 4, m16 = lane & 15;
   const int nb = A.K / QK_K;
   float mn = 1.f, rm = 1.f;
-  const bool norm = A.prologue == PRO_RMSNORM;
+  const bool norm = NM < 0 ? A.prologue == PRO_RMSNORM : NM == 1;
   if (norm) {
     mn = rms_denominator<true>(A, p, L.red);
     rm = 1.f / mn;
@@ -253,11 +256,12 @@ __device__ __forceinline__ void prologue_q8k(const GemvArgs& A, const XPre& p, c
 }
 
 // Q8_0 activation quantization (BlockQ8_0::from_float): 8 lanes per 32-block.
+template <int NM = -1>
 __device__ __forceinline__ void prologue_q80(const GemvArgs& A, const XPre& p, const Lds& L) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int nb = A.K / 256;
   float m = 1.f, rm = 1.f;
-  const bool norm = A.prologue == PRO_RMSNORM;
+  const bool norm = NM < 0 ? A.prologue == PRO_RMSNORM : NM == 1;
   if (norm) {
     m = rms_denominator<false>(A, p, L.red);
     rm = 1.f / m;
@@ -352,8 +356,10 @@ __device__ __forceinline__ float dot_group(const Raw<TPT_TYPE_Q4_K>& r, const Ac
     s0 = sdot4((int)(w[i] & 0x0F0F0F0Fu), a.q[i], s0);
     s1 = sdot4((int)((w[i] >> 4) & 0x0F0F0F0Fu), a.q[8 + i], s1);
   }
-  const int isum = sc0 * s0 + sc1 * s1;
-  const int msum = m0 * a.s[0] + m1 * a.s[1];
+  // 6-bit scales times sums of at most 64 products of 4-bit and 8-bit values: 24-bit multiplies
+  // are exact
+  const int isum = __mul24(sc0, s0) + __mul24(sc1, s1);
+  const int msum = __mul24(m0, a.s[0]) + __mul24(m1, a.s[1]);
   const float dd = h2f((uint16_t)(r.h.x & 0xffff)) * a.d0;
   const float dm = h2f((uint16_t)(r.h.x >> 16)) * a.d0;
   return dd * (float)isum - dm * (float)msum;
@@ -382,8 +388,9 @@ __device__ __forceinline__ float dot_group(const Raw<TPT_TYPE_Q6_K>& r, const Ac
   const uint32_t slo = r.sc.x >> (8 * h), shi = r.sc.y >> (8 * h);
   const int sc0 = (int8_t)(slo & 0xff), sc1 = (int8_t)((slo >> 16) & 0xff);
   const int sc2 = (int8_t)(shi & 0xff), sc3 = (int8_t)((shi >> 16) & 0xff);
-  const int isum = sc0 * (d0 - 32 * a.s[0]) + sc1 * (d1 - 32 * a.s[1]) +
-                   sc2 * (d2 - 32 * a.s[2]) + sc3 * (d3 - 32 * a.s[3]);
+  // |d - 32 s| < 2^18 and |sc| <= 128: 24-bit multiplies are exact
+  const int isum = __mul24(sc0, d0 - 32 * a.s[0]) + __mul24(sc1, d1 - 32 * a.s[1]) +
+                   __mul24(sc2, d2 - 32 * a.s[2]) + __mul24(sc3, d3 - 32 * a.s[3]);
   return (h2f((uint16_t)r.d) * a.d0) * (float)isum;
 }
 
@@ -426,15 +433,33 @@ struct NoHook {
 // One workgroup's share of a GEMV: rows [wg * rows_per_wg, ...).  WT weight type; BPP
 // super-blocks per row per pass (16, or fewer for short rows, then RPP = 16/BPP rows share a
 // pass); RB row slots per step; NMAT matrices (2: gate|up); KS-way split of the passes across
-// waves; D steps in flight per wave.  hook() runs after the activation and the first weight loads are issued, before the activation
-// is quantized.
-template <int WT, int BPP, int RB, int NMAT, int KS, int D, typename Hook>
+// waves; D steps in flight per wave; NORM: RMSNorm prologue; ONEPASS: one pass per row (the
+// lane's activation slice is then the same at every step and is read from LDS once).  hook()
+// runs after the activation and the first weight loads are issued, before the activation is
+// quantized.
+//
+// Row totals: a row's LPR lanes first reduce in 16-lane DPP rows; the NPART partial sums of a
+// row go to LDS and the epilogue adds them as (p0 + p1) + (p2 + p3) -- the bits a full
+// lane_group_sum<LPR> would give, without LDS round trips inside the step loop.
+template <int BPP> struct RowParts {
+  static constexpr int LPR = 4 * BPP;
+  static constexpr int N = LPR >= 16 ? LPR / 16 : 1;
+};
+template <int NPART>
+__device__ __forceinline__ float row_total(const float* p) {
+  if constexpr (NPART == 4) return (p[0] + p[1]) + (p[2] + p[3]);
+  else if constexpr (NPART == 2) return p[0] + p[1];
+  else return p[0];
+}
+
+template <int WT, int BPP, int RB, int NMAT, int KS, int D, bool NORM, bool ONEPASS, typename Hook>
 __device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int wg, char* smem,
                                          const Hook& hook) {
   constexpr int RPP = 16 / BPP;   // rows per pass
   constexpr int LPR = 4 * BPP;    // lanes per row
   constexpr int RG = RB * RPP;    // rows per row group
   constexpr int WR = NW / KS;     // waves per k-split
+  constexpr int NPART = RowParts<BPP>::N;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int K = A.K, N = A.N;
   const bool q80 = WT == TPT_TYPE_Q8_0;
@@ -478,16 +503,42 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int 
         load_raw<WT>((m == 0 ? A.w0 : A.w1) + (size_t)row * A.row_stride, g, buf[j][m]);
     }
   };
-  // 1. activation values first: the loads complete in issue order, so the prologue below only
+  // 0. the epilogue's own operands (residual, step position, argmax slot) are read before
+  //    everything else: their latency then hides under the weight stream instead of following it
+  const int nrows = min(RPW, N - r0);
+  float pre_r = 0.f;  // EPI_RESID: resid of row tid
+  int pos = 0, slot = 0;
+  if (A.epilogue == EPI_RESID && tid < nrows) pre_r = A.resid[r0 + tid];
+  if (A.epilogue == EPI_ROPE_QKV) pos = A.state ? A.state->pos : A.pos_host;
+  if (A.epilogue == EPI_ARGMAX) slot = A.state ? A.state->parity : 0;
+  // 1. activation values next: the loads complete in issue order, so the prologue below only
   //    waits for these, not for the weights issued after them
   XPre xp;
-  preload_x<WT != TPT_TYPE_Q8_0>(A, xp);
+  preload_x<WT != TPT_TYPE_Q8_0, NORM>(A, xp);
+  // every activation load ahead of every weight load, and no prologue arithmetic among them:
+  // the prologue then waits only for the former (left alone, the scheduler sinks some
+  // activation loads below the weight loads, or hoists the first uses of x above them)
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int d = 0; d < D; d++) issue(ring[d], d);
+  __builtin_amdgcn_sched_barrier(0);
   hook();
-  if constexpr (WT == TPT_TYPE_Q8_0) prologue_q80(A, xp, L);
-  else prologue_q8k(A, xp, L);
+  if constexpr (WT == TPT_TYPE_Q8_0) prologue_q80<NORM ? 1 : 0>(A, xp, L);
+  else prologue_q8k<NORM ? 1 : 0>(A, xp, L);
   barrier_lds();
+
+  // EPI_ROPE_QKV: the rotation of the thread's first (even, odd) row pair, issued behind the
+  // first weight steps (the position arrived with the activation)
+  float pre_c = 1.f, pre_s = 0.f;
+  if (A.epilogue == EPI_ROPE_QKV && 2 * tid < nrows) {
+    const int lrow = A.row0 + r0 + 2 * tid;
+    if (lrow < A.qd + A.kd) {
+      const int rr = lrow < A.qd ? lrow : lrow - A.qd;
+      const size_t ti = (size_t)pos * (A.hd / 2) + ((rr % A.hd) >> 1);
+      pre_c = A.rope_cos[ti];
+      pre_s = A.rope_sin[ti];
+    }
+  }
 
   float acc[RB][NMAT];
 #pragma unroll
@@ -495,12 +546,8 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int 
 #pragma unroll
     for (int m = 0; m < NMAT; m++) acc[j][m] = 0.f;
 
-  auto compute = [&](const Raw<WT> (&buf)[RB][NMAT], int s) {
+  auto compute = [&](const Raw<WT> (&buf)[RB][NMAT], int s, const Act& act, int g, bool v) {
     const int grp = wr + (s / PP) * WR, p = pa + s % PP;
-    bool v;
-    const int g = group_of(p, &v);
-    Act act;
-    load_act<WT>(L, g, act);
 #pragma unroll
     for (int j = 0; j < RB; j++)
 #pragma unroll
@@ -508,37 +555,63 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int 
         const float t = dot_group(buf[j][m], act, g);
         acc[j][m] += v ? t : 0.f;
       }
-    if (p == pb - 1) {  // row group done: row totals to LDS
+    if (p == pb - 1) {  // row group done: the row's partial sums to LDS
 #pragma unroll
       for (int j = 0; j < RB; j++)
 #pragma unroll
         for (int m = 0; m < NMAT; m++) {
-          const float t = lane_group_sum<LPR>(acc[j][m]);
-          if (lane % LPR == 0) L.rows[((size_t)ks * RPW + (grp * RB + j) * RPP + rp) * NMAT + m] = t;
+          float t;
+          int part = 0;
+          if constexpr (LPR >= 16) {
+            t = sum16(acc[j][m]);
+            part = (lane % LPR) >> 4;
+          } else {
+            t = lane_group_sum<LPR>(acc[j][m]);
+          }
+          if (lane % (LPR >= 16 ? 16 : LPR) == 0)
+            L.rows[(((size_t)ks * RPW + (grp * RB + j) * RPP + rp) * NMAT + m) * NPART + part] = t;
           acc[j][m] = 0.f;
         }
     }
   };
 
   if (S > 0) {
-    for (int s = 0; s < S; s += D) {
+    if constexpr (ONEPASS) {  // this lane's activation slice is the same at every step
+      bool v;
+      const int g = group_of(pa, &v);
+      Act act;
+      load_act<WT>(L, g, act);
+      for (int s = 0; s < S; s += D) {
 #pragma unroll
-      for (int d = 0; d < D; d++) {
-        if (s + d < S) compute(ring[d], s + d);
-        issue(ring[d], s + d + D);  // unconditional: the slot's next step
+        for (int d = 0; d < D; d++) {
+          if (s + d < S) compute(ring[d], s + d, act, g, v);
+          issue(ring[d], s + d + D);  // unconditional: the slot's next step
+        }
+      }
+    } else {
+      for (int s = 0; s < S; s += D) {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+          if (s + d < S) {
+            bool v;
+            const int g = group_of(pa + (s + d) % PP, &v);
+            Act act;
+            load_act<WT>(L, g, act);
+            compute(ring[d], s + d, act, g, v);
+          }
+          issue(ring[d], s + d + D);
+        }
       }
     }
   }
   __syncthreads();
 
-  // 3. epilogue over the workgroup's rows
-  const int nrows = min(RPW, N - r0);
-  int pos = 0;
-  if (A.epilogue == EPI_ROPE_QKV) pos = A.state ? A.state->pos : A.pos_host;
+  // 3. epilogue over the workgroup's rows (first row / pair of each thread from the operands
+  //    fetched up front)
   auto row_val = [&](int i, int m) {
     float t = 0.f;
 #pragma unroll
-    for (int k = 0; k < KS; k++) t += L.rows[((size_t)k * RPW + i) * NMAT + m];
+    for (int k = 0; k < KS; k++) t += row_total<NPART>(L.rows + (((size_t)k * RPW + i) * NMAT + m) * NPART);
     return t;
   };
   switch (A.epilogue) {
@@ -546,7 +619,12 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int 
       for (int i = tid; i < nrows; i += NT) A.y[r0 + i] = row_val(i, 0);
       break;
     case EPI_RESID:
-      for (int i = tid; i < nrows; i += NT) A.y[r0 + i] = row_val(i, 0) + A.resid[r0 + i];
+      for (int i = tid; i < nrows; i += NT) {
+        float r;
+        if (i == tid) r = pre_r;
+        else r = A.resid[r0 + i];
+        A.y[r0 + i] = row_val(i, 0) + r;
+      }
       break;
     case EPI_SWIGLU:
       for (int i = tid; i < nrows; i += NT) {
@@ -577,7 +655,7 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int 
         unsigned long long b = 0;
 #pragma unroll
         for (int w = 0; w < NW; w++) b = wbest[w] > b ? wbest[w] : b;
-        if (b) atomicMax(A.amax + (A.state ? A.state->parity : 0), b);
+        if (b) atomicMax(A.amax + slot, b);
       }
     } break;
     case EPI_ROPE_QKV:
@@ -589,7 +667,14 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int 
           const bool isq = lrow < A.qd;
           const int rr = isq ? lrow : lrow - A.qd;
           const size_t ti = (size_t)pos * (A.hd / 2) + ((rr % A.hd) >> 1);
-          const float cs = A.rope_cos[ti], sn = A.rope_sin[ti];
+          float cs, sn;
+          if (i == 2 * tid) {
+            cs = pre_c;
+            sn = pre_s;
+          } else {
+            cs = A.rope_cos[ti];
+            sn = A.rope_sin[ti];
+          }
           // candle rope_i: dst[2i] = x0*cos - x1*sin; dst[2i+1] = x0*sin + x1*cos
           const float o0 = x0 * cs - x1 * sn, o1 = x0 * sn + x1 * cs;
           if (isq) {

@@ -42,10 +42,22 @@ namespace {
 
 using namespace gemv;
 
-template <int WT, int BPP, int RB, int NMAT, int KS, int D>
+template <int WT, int BPP, int RB, int NMAT, int KS, int D, bool NORM, bool ONEPASS>
 __global__ void __launch_bounds__(NT, 1) gemv_q8_kernel(const GemvArgs A, const Geo geo) {
   extern __shared__ __align__(16) char smem[];
-  gemv_run<WT, BPP, RB, NMAT, KS, D>(A, geo, blockIdx.x, smem, NoHook());
+  gemv_run<WT, BPP, RB, NMAT, KS, D, NORM, ONEPASS>(A, geo, blockIdx.x, smem, NoHook());
+}
+
+// The launch of one instantiation (ev0/ev1: dispatch-stamped events, hipExtLaunchKernelGGL).
+template <int WT, int BPP, int RB, int NMAT, int KS, int D, bool NORM, bool ONEPASS>
+void launch_inst(const GemvArgs& a, const Geo& geo, int grid, size_t lds, hipStream_t s, hipEvent_t ev0,
+                 hipEvent_t ev1) {
+  if (ev0 || ev1)
+    hipExtLaunchKernelGGL((gemv_q8_kernel<WT, BPP, RB, NMAT, KS, D, NORM, ONEPASS>), dim3((unsigned)grid),
+                          dim3(NT), lds, s, ev0, ev1, 0, a, geo);
+  else
+    hipLaunchKernelGGL((gemv_q8_kernel<WT, BPP, RB, NMAT, KS, D, NORM, ONEPASS>), dim3((unsigned)grid),
+                       dim3(NT), lds, s, a, geo);
 }
 
 // ----------------------------------------------------------------- fp32-activation variant
@@ -173,13 +185,13 @@ int launch_cfg(const tpt_ctx* ctx, const GemvArgs& a, int wg_per_cu, hipStream_t
   rpw = (rpw + unit - 1) / unit * unit;
   geo.rows_per_wg = rpw;
   const int grid = (a.N + rpw - 1) / rpw;
-  const size_t lds = lds_act_bytes(a.K, WT == TPT_TYPE_Q8_0) + 4 * (size_t)KS * rpw * NMAT;
+  const size_t lds = lds_act_bytes(a.K, WT == TPT_TYPE_Q8_0) + 4 * (size_t)KS * rpw * NMAT * RowParts<BPP>::N;
   if (lds > 65536) return fail(TPT_ERR_UNSUPPORTED, "gemv: too many rows per workgroup for LDS");
-  if (ev0 || ev1)  // the dispatch itself timestamps the events (no packets between kernels)
-    hipExtLaunchKernelGGL((gemv_q8_kernel<WT, BPP, RB, NMAT, KS, D>), dim3((unsigned)grid), dim3(NT), lds, s,
-                          ev0, ev1, 0, a, geo);
-  else
-    hipLaunchKernelGGL((gemv_q8_kernel<WT, BPP, RB, NMAT, KS, D>), dim3((unsigned)grid), dim3(NT), lds, s, a, geo);
+  const bool norm = a.prologue == PRO_RMSNORM, one = geo.P == KS;  // one pass per k-split wave
+  if (norm && one) launch_inst<WT, BPP, RB, NMAT, KS, D, true, true>(a, geo, grid, lds, s, ev0, ev1);
+  else if (norm) launch_inst<WT, BPP, RB, NMAT, KS, D, true, false>(a, geo, grid, lds, s, ev0, ev1);
+  else if (one) launch_inst<WT, BPP, RB, NMAT, KS, D, false, true>(a, geo, grid, lds, s, ev0, ev1);
+  else launch_inst<WT, BPP, RB, NMAT, KS, D, false, false>(a, geo, grid, lds, s, ev0, ev1);
   TPT_HIP(hipGetLastError());
   return TPT_OK;
 }

@@ -102,7 +102,7 @@ EXPORTS = {
     "tpt_engine_reset_cache": ([P], I32),
     "tpt_common_prefix_len": ([P, SZ, P, SZ], SZ),
     "tpt_bench_gemv": ([P, I32, P, I32, P, P, I32, I32, I32, P], I32),
-    "tpt_bench_attn": ([P, P, P, P, I32, P, I32, I32, I32, I32, I32, I32, I32, P], I32),
+    "tpt_bench_attn": ([P, P, P, P, I32, I32, P, I32, I32, I32, I32, I32, I32, I32, P], I32),
     "tpt_bench_copy": ([P, P, P, SZ, I32, P], I32),
     "tpt_gemm": ([P, I32, P, P, P, I32, I32, I32, I32], I32),
     "tpt_bench_gemm": ([P, I32, P, P, P, I32, I32, I32, I32, I32, P], I32),
@@ -265,11 +265,16 @@ class Context:
                                     hd, L, L_stride, n_chunks))
         return o.download(np.float32, nq * hd)
 
-    def bench_attn(self, qbuf, kbuf, vbuf, obuf, nq, nkv, hd, L, L_stride, iters, n_chunks=0,
+    def bench_attn(self, qbuf, kbufs, vbufs, obuf, nq, nkv, hd, L, L_stride, iters, n_chunks=0,
                    kv_type=TYPE_F16):
-        """Event-timed back-to-back decode-attention launches over one cache; returns ms."""
+        """Event-timed back-to-back decode-attention launches, launch i over the caches
+        kbufs[i % n] / vbufs[i % n]; returns ms."""
+        ks = (C.c_void_p * len(kbufs))(*[b.ptr for b in kbufs])
+        vs = (C.c_void_p * len(vbufs))(*[b.ptr for b in vbufs])
+        if len(kbufs) != len(vbufs):
+            raise ValueError("bench_attn: as many K caches as V caches")
         ms = C.c_float()
-        check(lib().tpt_bench_attn(self.h, qbuf.ptr, kbuf.ptr, vbuf.ptr, kv_type, obuf.ptr, nq, nkv,
+        check(lib().tpt_bench_attn(self.h, qbuf.ptr, ks, vs, len(kbufs), kv_type, obuf.ptr, nq, nkv,
                                    hd, L, L_stride, n_chunks, iters, C.byref(ms)))
         return ms.value
 
