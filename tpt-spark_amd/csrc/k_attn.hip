@@ -51,14 +51,11 @@ __global__ void __launch_bounds__(ANT) attn_partial_kernel(const AttnArgs a, con
   const int li = tid % LPP, pg = tid / LPP;  // lane in position, position group 0..R-1
   const int kvh = blockIdx.y, chunk = blockIdx.x, nch = gridDim.x, t = blockIdx.z;
   // The chunk's rows are known at launch; the live length L (from the step state on the
-  // decode path) only masks, so the K/V loads do not wait for it.
+  // decode path) only masks: q and the first round's K and V rows are requested before L is
+  // read, so no load waits for it (a chunk past L discards what it fetched).
   const int CL = a.chunk_len;
   const int p0 = chunk * CL;
   const int plast = min(p0 + CL, a.L_stride) - 1;  // clamped loads stay inside the cache
-  const int L = (a.state ? a.state->pos + 1 : a.L_host) + t;
-  const int p1 = min(L, p0 + CL);
-  const int n = p1 - p0;
-  if (n <= 0) return;  // a chunk past the live length: the merge does not read its record
 
   const T* K = (const T*)a.kc + (size_t)kvh * a.L_stride * HD + li * EPL;
   const T* V = (const T*)a.vc + (size_t)kvh * a.L_stride * HD + li * EPL;
@@ -68,25 +65,31 @@ __global__ void __launch_bounds__(ANT) attn_partial_kernel(const AttnArgs a, con
   for (int h = 0; h < G; h++)
 #pragma unroll
     for (int e = 0; e < EPL; e++) q[h][e] = a.q[(size_t)t * a.ldq + (size_t)(kvh * G + h) * HD + li * EPL + e];
+  float k0[U][EPL], vpre[U][EPL];
+#pragma unroll
+  for (int u = 0; u < U; u++) load_row<EPL>(K + (size_t)min(p0 + u * R + pg, plast) * HD, k0[u]);
+#pragma unroll
+  for (int u = 0; u < U; u++) load_row<EPL>(V + (size_t)min(p0 + u * R + pg, plast) * HD, vpre[u]);
 
-  // phase 1: scores (the first round also fetches its V rows)
-  float vpre[U][EPL];
+  const int L = (a.state ? a.state->pos + 1 : a.L_host) + t;
+  const int p1 = min(L, p0 + CL);
+  const int n = p1 - p0;
+  if (n <= 0) return;  // a chunk past the live length: the merge does not read its record
+
+  // phase 1: scores
   float mloc[G];
 #pragma unroll
   for (int h = 0; h < G; h++) mloc[h] = -INFINITY;
-  for (int base = p0; base < p0 + CL && base < L; base += R * U) {
+  for (int base = p0; base < p1; base += R * U) {
     float k[U][EPL];
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-      const int p = min(base + u * R + pg, plast);
-      load_row<EPL>(K + (size_t)p * HD, k[u]);
-    }
     if (base == p0) {
 #pragma unroll
-      for (int u = 0; u < U; u++) {
-        const int p = min(base + u * R + pg, plast);
-        load_row<EPL>(V + (size_t)p * HD, vpre[u]);
-      }
+      for (int u = 0; u < U; u++)
+#pragma unroll
+        for (int e = 0; e < EPL; e++) k[u][e] = k0[u][e];
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; u++) load_row<EPL>(K + (size_t)min(base + u * R + pg, plast) * HD, k[u]);
     }
 #pragma unroll
     for (int u = 0; u < U; u++) {
@@ -106,7 +109,7 @@ __global__ void __launch_bounds__(ANT) attn_partial_kernel(const AttnArgs a, con
   }
 #pragma unroll
   for (int h = 0; h < G; h++) {
-    const float m = wave_max(mloc[h]);
+    const float m = wave_max_dpp(mloc[h]);
     if (lane == 0) s_red[wid][h] = m;
   }
   __syncthreads();
@@ -128,7 +131,7 @@ __global__ void __launch_bounds__(ANT) attn_partial_kernel(const AttnArgs a, con
       s_p[h][j] = w;
       ls += w;
     }
-    ls = wave_sum(ls);
+    ls = wave_sum_dpp(ls);
     if (lane == 0) s_red[wid][h] = ls;
   }
   __syncthreads();
@@ -221,7 +224,7 @@ __global__ void __launch_bounds__(ANT) attn_merge_kernel(const float* __restrict
   if (tid < WAVE) {
     float mm = -INFINITY;
     for (int c = lane; c < nch; c += WAVE) mm = fmaxf(mm, pk[(size_t)c * G * PSTRIDE + HD]);
-    mm = wave_max(mm);
+    mm = wave_max_dpp(mm);
     float ls = 0.f;
     for (int c = lane; c < nch; c += WAVE) {
       const float* rec = pk + (size_t)c * G * PSTRIDE;
@@ -229,7 +232,7 @@ __global__ void __launch_bounds__(ANT) attn_merge_kernel(const float* __restrict
       s_w[c] = w;
       ls = fmaf(w, rec[HD + 1], ls);
     }
-    ls = wave_sum(ls);
+    ls = wave_sum_dpp(ls);
     if (lane == 0) s_l = ls;
   }
   __syncthreads();

@@ -445,7 +445,7 @@ struct Att {
     }
 #pragma unroll
     for (int h = 0; h < G; h++) {
-      const float m = wave_max(mloc[h]);
+      const float m = wave_max_dpp(mloc[h]);
       if (lane == 0) s_red[hw * G + h] = m;
     }
     barrier_lds();
@@ -462,7 +462,7 @@ struct Att {
         s_p[h * CL + j] = w;
         ls += w;
       }
-      ls = wave_sum(ls);
+      ls = wave_sum_dpp(ls);
       if (lane == 0) s_red[hw * G + h] = ls;
     }
     barrier_lds();
@@ -655,7 +655,7 @@ __device__ __noinline__ unsigned ph_mrg(int pos, unsigned e) {
       const float mv = s2 ? m_hi : m_lo, lv = s2 ? l_hi : l_lo;
       float mm = lane < nact ? mv : -INFINITY;
       for (int c = lane + WAVE; c < nact; c += WAVE) mm = fmaxf(mm, ldb(rp, 4u * (rec(c, hh) + HD)));
-      mm = wave_max(mm);
+      mm = wave_max_dpp(mm);
       float ls = 0.f;
       if (lane < nact) {
         const float w = expf(mv - mm);
@@ -667,7 +667,7 @@ __device__ __noinline__ unsigned ph_mrg(int pos, unsigned e) {
         wbuf[s2 * nch + c] = w;
         ls = fmaf(w, ldb(rp, 4u * (rec(c, hh) + HD + 1)), ls);
       }
-      lsum[s2] = wave_sum(ls);
+      lsum[s2] = wave_sum_dpp(ls);
     }
     if (i <= ilast) {
       const bool lo = h == hlo;
