@@ -17,6 +17,10 @@ context's stream, over back-to-back launches that rotate through distinct weight
 (> 1 GB, more than the 256 MB Infinity Cache).  Algorithmic bytes per launch =
 K*N*144/256 + 4K + 4N.  traffic comes from the committed rocprofv3 PMC summary when present.
 
+Further legs reported in `config` (not the headline): decode attention at the long-context
+shapes (`attn_decode_f16`, GB/s vs HBM peak over rotating caches) and the MFMA prefill GEMM at the
+prompt shapes (`prefill_gemm_q4k`, TFLOP/s vs the 2.5 PFLOP/s dense fp16 peak).
+
 cpu_baseline: the CPU oracle's restatement of candle's CPU decode (Q8_K activation quant,
 integer vec_dot, OpenMP over output columns) timed on this host's cores on a bounded sample of
 the same model: a short prompt, then greedy decode steps for about 20 s.
@@ -113,6 +117,35 @@ def attn_roofline(tp, ctx, iters=64):
     return out
 
 
+# prefill GEMM shapes: M prompt rows, K = 4096, N = 4096 (Q/O) and 14336 (gate/up)
+GEMM_CASES = [(M, 4096, N) for M in (128, 512, 2048) for N in (4096, 14336)]
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def gemm_roofline(tp, ctx, iters=20):
+    """MFMA prefill GEMM Y[M,N] = X[M,K] . W[N,K]^T (W Q4_K) at GEMM_CASES, both activation modes:
+    "q8k" (candle's arithmetic, the model's prefill) and "f16".  Each mode runs on fp16 MFMA
+    (dense peak 2.5 PFLOP/s); flops per launch = 2 M N K; time = mean of the dispatch-stamped
+    event intervals of `iters` launches after one untimed launch."""
+    from tpthip import synth
+    out = {}
+    for M, K, N in GEMM_CASES:
+        w = ctx.to_device(synth.random_weights(tp.TYPE_Q4_K, N, K, seed=N + 3, name=f"gemm{N}"))
+        x = ctx.to_device(np.random.default_rng(M).standard_normal((M, K), dtype=np.float32))
+        y = ctx.alloc(M * N * 4)
+        for mode, act in (("q8k", tp.ACT_Q8), ("f16", tp.ACT_F16)):
+            ctx.bench_gemm(tp.TYPE_Q4_K, w, x, y, M, K, N, 1, act=act)
+            ms = ctx.bench_gemm(tp.TYPE_Q4_K, w, x, y, M, K, N, iters, act=act)
+            us = ms * 1e3 / iters
+            tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
+            out[f"{mode} {M}x{K}x{N}"] = {"us_per_launch": round(us, 2), "tflops": round(tf, 1),
+                                          "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}
+            log(f"gemm {mode} M={M} K={K} N={N}: {us:.1f} us/launch, {tf:.1f} TFLOP/s")
+        for b in (w, x, y):
+            b.free()
+    return out
+
+
 def cpu_baseline(path, budget_s=20.0):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
@@ -161,9 +194,9 @@ def main():
     ap.add_argument("--prompt", type=int, default=PROMPT_LEN)
     ap.add_argument("--model", default="", help="existing GGUF (default: generate the 8B shape)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--leg", choices=["all", "gemv", "attn"], default="all",
+    ap.add_argument("--leg", choices=["all", "gemv", "attn", "gemm"], default="all",
                     help="gemv: only the GEMV roofline leg and the copy calibration (profiling); "
-                         "attn: only the decode-attention leg")
+                         "attn: only the decode-attention leg; gemm: only the prefill GEMM leg")
     ap.add_argument("--gemv-iters", type=int, default=256, help="timed launches per GEMV shape")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -180,11 +213,15 @@ def main():
     if args.leg == "attn":
         print(json.dumps({"attn_decode": attn_roofline(tp, ctx)}))
         return
+    if args.leg == "gemm":
+        print(json.dumps({"prefill_gemm": gemm_roofline(tp, ctx)}))
+        return
     gemv = gemv_roofline(tp, ctx, iters=args.gemv_iters)
     if args.leg == "gemv":
         print(json.dumps({"gemv": gemv, "copy": copy_calibration(ctx)}))
         return
     attn = attn_roofline(tp, ctx)
+    gemm = gemm_roofline(tp, ctx)
 
     tmpdir = tempfile.mkdtemp(prefix="tpt_bench_", dir=os.environ.get("TPT_BENCH_DIR") or None)
     path = args.model
@@ -262,6 +299,7 @@ def main():
             "arith": "q4_k/q6_k weights x q8_k activations: int8 dot4 -> int32, f32 block scales",
             "gemv_q4k": gemv,
             "attn_decode_f16": attn,
+            "prefill_gemm_q4k": gemm,
         },
         "roofline": {
             "bound": "hbm",
