@@ -299,17 +299,18 @@ int gemm_prepare(tpt_ctx* c, int type, const void* w, const float* x, float* y, 
   ActPrepArgs p;
   p.M = M; p.K = K; p.ldx = K; p.x = x; p.mode = g.mode;
   const size_t mk = (size_t)M * K;
-  const size_t bytes = g.mode == GEMM_Q8K ? mk + (size_t)M * (K / 256) * 4 + (size_t)M * (K / 16) * 2 + 512 : mk * 2 + 256;
+  // fp16 rows [M][K], then (GEMM_Q8K) block scales [M][K/256] and per-16 sums [M][K/16]
+  const size_t o_d = (mk * 2 + 255) & ~(size_t)255;
+  const size_t o_s = o_d + (((size_t)M * (K / 256) * 4 + 255) & ~(size_t)255);
+  const size_t bytes = g.mode == GEMM_Q8K ? o_s + (size_t)M * (K / 16) * 2 : mk * 2;
   TPT_HIP(hipMallocAsync(&call->scratch, bytes, c->stream));
   uint8_t* base = (uint8_t*)call->scratch;
+  p.af = (uint16_t*)base;
+  g.af = p.af;
   if (g.mode == GEMM_Q8K) {
-    p.aq = (int8_t*)base;
-    p.ad = (float*)(base + ((mk + 255) & ~(size_t)255));
-    p.as16 = (int16_t*)(base + ((mk + 255) & ~(size_t)255) + (((size_t)M * (K / 256) * 4 + 255) & ~(size_t)255));
-    g.aq = p.aq; g.ad = p.ad; g.as16 = p.as16;
-  } else {
-    p.af = (uint16_t*)base;
-    g.af = p.af;
+    p.ad = (float*)(base + o_d);
+    p.as16 = (int16_t*)(base + o_s);
+    g.ad = p.ad; g.as16 = p.as16;
   }
   int rc = launch_act_prep(p, c->stream);
   if (rc) (void)hipFreeAsync(call->scratch, c->stream);

@@ -16,8 +16,12 @@
 //  * GEMM_F16: the tile is dequantized into LDS as fp16 (d*sc*q - dmin*m rounded to fp16), the
 //    activation is fp16, one fp32 MFMA chain over all of K.
 // Tiling (MI355X: 160 KB LDS, wave64, v_mfma_f32_32x32x16_f16): 256 threads, a 128 x 128 tile
-// of Y per workgroup, each wave 64 x 64 (2 x 2 MFMA tiles), K stepped one super-block (256) at
-// a time through LDS; the next step's global loads are issued before the current step's MFMAs.
+// of Y per workgroup, each wave 64 x 64 (2 x 2 MFMA tiles).  K advances half a super-block (128)
+// per step through a double-buffered LDS tile: while a step's MFMAs read one buffer, the next
+// step's weights are decoded into the other and the step after that is in flight from HBM, so
+// the Q4_K decode overlaps the matrix cores instead of alternating with them.  The activation
+// arrives as fp16 rows from act_prep_kernel (in GEMM_Q8K mode the int8 values, exact in fp16), so
+// no workgroup converts it again.
 #include <hip/hip_ext.h>
 
 #include "kernels.h"
@@ -27,37 +31,42 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+// native 16-byte vector (HIP's uint4 is a struct: its copies go through private memory)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int GT = 256;          // threads per workgroup
-constexpr int BM = 128, BN = 128, BK = 256;
+constexpr int BM = 128, BN = 128, BK = 128;
 constexpr int LDK = BK + 8;      // fp16 per LDS row (16 B pad: conflict-free 16-byte reads)
-constexpr int LDG = 16 + 8;      // per-16 sums / mins row
+constexpr int LDG = 16;          // per-16 sums / mins row
 
-struct GemmSmem {
+struct GemmTile {                // one K step's operands
   _Float16 a[BM][LDK];
   _Float16 b[BN][LDK];
-  _Float16 a16[BM][LDG];  // Q8K: activation per-16 sums of the block
-  _Float16 b16[BN][LDG];  // Q8K: weight mins, each repeated for its two 16-element halves
-  float dx[BM];           // Q8K: activation block scale
-  float dw[BN], dm[BN];   // Q8K: weight d, dmin
+};
+struct GemmBlock {               // GEMM_Q8K: one super-block's per-row and per-column data
+  _Float16 a16[BM][LDG];         // activation per-16 sums
+  _Float16 b16[BN][LDG];         // weight mins, each repeated for its two 16-element halves
+  float dx[BM];                  // activation block scale
+  float dw[BN], dm[BN];          // weight d, dmin
+};
+struct GemmSmem {
+  GemmTile t[2];                 // by step parity: the half of the super-block
+  GemmBlock blk[2];              // by super-block parity
 };
 
-// registers one thread stages for a K-step: 128 activation values and half a weight block
-template <int MODE> struct Stage;
-template <> struct Stage<GEMM_Q8K> {
-  uint4 a[8];   // 128 int8
-  uint4 a16;    // 8 per-16 sums (int16)
-  float dx;     // block scale
-  uint4 h;      // weight block header
-  uint4 q[4];   // 64 qs bytes (half a block)
-};
-template <> struct Stage<GEMM_F16> {
-  uint4 a[16];  // 128 fp16
-  uint4 h;
-  uint4 q[4];
+// Registers one thread stages for a K step (thread = row r, half hf of the step's 128 elements,
+// which is one 64-weight Q4_K group): 64 fp16 activation values, the weight block header, the
+// group's 32 qs bytes; in the first half of a super-block also 8 of the row's per-16 sums and
+// its block scale.
+struct Stage {
+  u32x4 a[8];
+  u32x4 h;
+  u32x4 q[2];
+  u32x4 a16;
+  float dx;
 };
 
-__device__ __forceinline__ void get_scale_min(const uint4& h, int j, int* sc, int* m) {
+__device__ __forceinline__ void get_scale_min(const u32x4& h, int j, int* sc, int* m) {
   // get_scale_min_k4 (ggml/candle): scales bytes s[0..11] are h.y, h.z, h.w
   const uint32_t Y = h.y, Z = h.z, W = h.w;
   if (j < 4) {
@@ -70,122 +79,172 @@ __device__ __forceinline__ void get_scale_min(const uint4& h, int j, int* sc, in
   }
 }
 
-template <int MODE>
-__device__ __forceinline__ void stage_load(const GemmArgs& g, int m0, int n0, int kb, Stage<MODE>& st) {
+// step = 2 kb + hb: super-block kb, half hb
+template <int MODE, int HB>
+__device__ __forceinline__ void stage_load(const GemmArgs& g, int m0, int n0, int kb, Stage& st) {
   const int tid = threadIdx.x, r = tid >> 1, hf = tid & 1;
   int m = m0 + r;
   if (m >= g.M) m = g.M - 1;
   int n = n0 + r;
   if (n >= g.N) n = g.N - 1;
-  if constexpr (MODE == GEMM_Q8K) {
-    const uint4* src = (const uint4*)(g.aq + (size_t)m * g.K + (size_t)kb * 256 + 128 * hf);
+  const u32x4* src = (const u32x4*)(g.af + (size_t)m * g.K + (size_t)kb * 256 + 128 * HB + 64 * hf);
 #pragma unroll
-    for (int i = 0; i < 8; i++) st.a[i] = src[i];
-    st.a16 = *(const uint4*)(g.as16 + (size_t)m * (g.K / 16) + kb * 16 + 8 * hf);
-    st.dx = g.ad[(size_t)m * (g.K / 256) + kb];
-  } else {
-    const uint4* src = (const uint4*)(g.af + (size_t)m * g.K + (size_t)kb * 256 + 128 * hf);
-#pragma unroll
-    for (int i = 0; i < 16; i++) st.a[i] = src[i];
-  }
+  for (int i = 0; i < 8; i++) st.a[i] = src[i];
   const uint8_t* blk = g.w + (size_t)n * g.w_stride + (size_t)kb * 144;
-  st.h = *(const uint4*)blk;
-  const uint4* qs = (const uint4*)(blk + 16 + 64 * hf);
-#pragma unroll
-  for (int i = 0; i < 4; i++) st.q[i] = qs[i];
+  st.h = *(const u32x4*)blk;
+  const u32x4* qs = (const u32x4*)(blk + 16 + 32 * (2 * HB + hf));
+  st.q[0] = qs[0];
+  st.q[1] = qs[1];
+  if constexpr (MODE == GEMM_Q8K && HB == 0) {
+    st.a16 = *(const u32x4*)(g.as16 + (size_t)m * (g.K / 16) + kb * 16 + 8 * hf);
+    st.dx = g.ad[(size_t)m * (g.K / 256) + kb];
+  }
 }
 
-template <int MODE>
-__device__ __forceinline__ void stage_store(const Stage<MODE>& st, GemmSmem& s) {
+template <int MODE, int HB>
+__device__ __forceinline__ void stage_store(const Stage& st, GemmTile& T, GemmBlock& B) {
   const int tid = threadIdx.x, r = tid >> 1, hf = tid & 1;
-  // activation row r, elements 128 hf .. +128
-  if constexpr (MODE == GEMM_Q8K) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const uint32_t w[4] = {st.a[i].x, st.a[i].y, st.a[i].z, st.a[i].w};
-      half8 lo, hi;
+  for (int i = 0; i < 8; i++) *(u32x4*)&T.a[r][64 * hf + 8 * i] = st.a[i];
+  // weight row r, group g = 2 HB + hf: qs[32g + l] holds element 64g + l (low nibble, sub-block
+  // 2g) and 64g + 32 + l (high nibble, sub-block 2g + 1); in the step tile at 64 hf + l, + 32
+  const int g = 2 * HB + hf;
+  const float d = h2f((uint16_t)(st.h.x & 0xffff)), dmin = h2f((uint16_t)(st.h.x >> 16));
+  int sc0, m0, sc1, m1;
+  get_scale_min(st.h, 2 * g, &sc0, &m0);
+  get_scale_min(st.h, 2 * g + 1, &sc1, &m1);
+  const uint32_t w[8] = {st.q[0].x, st.q[0].y, st.q[0].z, st.q[0].w, st.q[1].x, st.q[1].y, st.q[1].z, st.q[1].w};
+  const int e0 = 64 * hf;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {  // 8 consecutive elements per half8 store
+    half8 lo, hi;
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+      const uint32_t byte = (w[2 * c + t / 4] >> (8 * (t % 4))) & 0xff;
+      const int ql = byte & 0xF, qh = byte >> 4;
+      if constexpr (MODE == GEMM_Q8K) {
+        lo[t] = (_Float16)(sc0 * ql);
+        hi[t] = (_Float16)(sc1 * qh);
+      } else {
+        const float d1 = d * (float)sc0, mm1 = dmin * (float)m0;
+        const float d2 = d * (float)sc1, mm2 = dmin * (float)m1;
+        lo[t] = (_Float16)(d1 * (float)ql - mm1);
+        hi[t] = (_Float16)(d2 * (float)qh - mm2);
+      }
+    }
+    *(half8*)&T.b[r][e0 + 8 * c] = lo;
+    *(half8*)&T.b[r][e0 + 32 + 8 * c] = hi;
+  }
+  if constexpr (MODE == GEMM_Q8K) {
+    // mins of sub-blocks 2g, 2g + 1, each for its two 16-element halves (16-sums 8g .. 8g+3)
+    B.b16[r][4 * g] = (_Float16)m0;
+    B.b16[r][4 * g + 1] = (_Float16)m0;
+    B.b16[r][4 * g + 2] = (_Float16)m1;
+    B.b16[r][4 * g + 3] = (_Float16)m1;
+    if constexpr (HB == 0) {
+      const uint32_t b[4] = {st.a16.x, st.a16.y, st.a16.z, st.a16.w};
+      half8 v;
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const _Float16 v0 = (_Float16)(int8_t)(w[j] & 0xff), v1 = (_Float16)(int8_t)((w[j] >> 8) & 0xff);
-        const _Float16 v2 = (_Float16)(int8_t)((w[j] >> 16) & 0xff), v3 = (_Float16)(int8_t)(w[j] >> 24);
-        if (j < 2) { lo[4 * j] = v0; lo[4 * j + 1] = v1; lo[4 * j + 2] = v2; lo[4 * j + 3] = v3; }
-        else { hi[4 * j - 8] = v0; hi[4 * j - 7] = v1; hi[4 * j - 6] = v2; hi[4 * j - 5] = v3; }
+        v[2 * j] = (_Float16)(int16_t)(b[j] & 0xffff);
+        v[2 * j + 1] = (_Float16)(int16_t)(b[j] >> 16);
       }
-      *(half8*)&s.a[r][128 * hf + 16 * i] = lo;
-      *(half8*)&s.a[r][128 * hf + 16 * i + 8] = hi;
+      *(half8*)&B.a16[r][8 * hf] = v;
+      // both threads of the row hold the same values: the duplicate stores keep the step one
+      // basic block for the scheduler
+      B.dx[r] = st.dx;
+      B.dw[r] = d;
+      B.dm[r] = dmin;
     }
-    const uint32_t b[4] = {st.a16.x, st.a16.y, st.a16.z, st.a16.w};
-    half8 v;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      v[2 * j] = (_Float16)(int16_t)(b[j] & 0xffff);
-      v[2 * j + 1] = (_Float16)(int16_t)(b[j] >> 16);
-    }
-    *(half8*)&s.a16[r][8 * hf] = v;
-    if (hf == 0) s.dx[r] = st.dx;
-  } else {
-#pragma unroll
-    for (int i = 0; i < 16; i++) *(uint4*)&s.a[r][128 * hf + 8 * i] = st.a[i];
   }
-  // weight row r, groups g = 2 hf, 2 hf + 1 (elements 128 hf .. +128): qs[32g + l] holds element
-  // 64g + l (low nibble, sub-block 2g) and 64g + 32 + l (high nibble, sub-block 2g + 1)
-  const float d = h2f((uint16_t)(st.h.x & 0xffff)), dmin = h2f((uint16_t)(st.h.x >> 16));
+}
+
+// Instruction interleave of one K step (one basic block: the staging of the next step and this
+// step's MFMAs): per 16-element slice of K, its operand reads and 4 MFMAs, then a share of the
+// staging work (the Q4_K decode's VALU, its LDS writes, the global loads of the step after), so
+// the decode runs while the matrix cores work instead of after them.
+__device__ __forceinline__ void interleave_step() {
 #pragma unroll
-  for (int gg = 0; gg < 2; gg++) {
-    const int g = 2 * hf + gg;
-    int sc0, m0, sc1, m1;
-    get_scale_min(st.h, 2 * g, &sc0, &m0);
-    get_scale_min(st.h, 2 * g + 1, &sc1, &m1);
-    const uint4 q0 = st.q[2 * gg], q1 = st.q[2 * gg + 1];
-    const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-    const int e0 = 64 * g;
+  for (int i = 0; i < BK / 16; i++) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // LDS reads (operands)
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x002, 48, 0); // VALU
+    __builtin_amdgcn_sched_group_barrier(0x200, 3, 0);  // LDS writes
+    __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // global loads
+  }
+}
+
+// One K step of MFMAs on tile T into acc (each wave: 64 x 64 as 2 x 2 tiles of 32 x 32).
+__device__ __forceinline__ void mfma_step(const GemmTile& T, floatx16 (&acc)[2][2]) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wm = wid >> 1, wn = wid & 1;
+  const int lr = lane & 31, lk = 8 * (lane >> 5);
 #pragma unroll
-    for (int c = 0; c < 4; c++) {  // 8 consecutive elements per half8 store
-      half8 lo, hi;
+  for (int kk = 0; kk < BK; kk += 16) {
+    half8 a[2], b[2];
 #pragma unroll
-      for (int t = 0; t < 8; t++) {
-        const uint32_t byte = (w[2 * c + t / 4] >> (8 * (t % 4))) & 0xff;
-        const int ql = byte & 0xF, qh = byte >> 4;
-        if constexpr (MODE == GEMM_Q8K) {
-          lo[t] = (_Float16)(sc0 * ql);
-          hi[t] = (_Float16)(sc1 * qh);
-        } else {
-          const float d1 = d * (float)sc0, mm1 = dmin * (float)m0;
-          const float d2 = d * (float)sc1, mm2 = dmin * (float)m1;
-          lo[t] = (_Float16)(d1 * (float)ql - mm1);
-          hi[t] = (_Float16)(d2 * (float)qh - mm2);
-        }
+    for (int i = 0; i < 2; i++) a[i] = *(const half8*)&T.a[64 * wm + 32 * i + lr][kk + lk];
+#pragma unroll
+    for (int j = 0; j < 2; j++) b[j] = *(const half8*)&T.b[64 * wn + 32 * j + lr][kk + lk];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+  }
+}
+
+// GEMM_Q8K end of a super-block: the mins term on the matrix cores (K = 16, exact), then per
+// element candle's f32 arithmetic y += (d_w d_x) isum - (dmin_w d_x) msum with isum = the two
+// exact 128-element chains added once (as (float)isum rounds in candle).
+__device__ __forceinline__ void block_end(const GemmBlock& B, floatx16 (&acc0)[2][2], floatx16 (&acc1)[2][2],
+                                          floatx16 (&out)[2][2]) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wm = wid >> 1, wn = wid & 1;
+  const int lr = lane & 31, lk = 8 * (lane >> 5);
+  half8 a[2], b[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++) a[i] = *(const half8*)&B.a16[64 * wm + 32 * i + lr][lk];
+#pragma unroll
+  for (int j = 0; j < 2; j++) b[j] = *(const half8*)&B.b16[64 * wn + 32 * j + lr][lk];
+  // the lane's 16 rows of tile i are 4 runs of 4 consecutive rows: one float4 each
+  float dxs[2][16];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const float4 v = *(const float4*)&B.dx[64 * wm + 32 * i + q * 8 + (lane >> 5) * 4];
+      dxs[i][4 * q] = v.x; dxs[i][4 * q + 1] = v.y; dxs[i][4 * q + 2] = v.z; dxs[i][4 * q + 3] = v.w;
+    }
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const floatx16 accm = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], floatx16{}, 0, 0, 0);
+      const int col = 64 * wn + 32 * j + lr;
+      const float dw = B.dw[col], dm = B.dm[col];
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const float dx = dxs[i][e];
+        const float isum = acc0[i][j][e] + acc1[i][j][e];
+        const float dd = dw * dx, ddm = dm * dx;
+        const float v = dd * isum - ddm * accm[e];
+        out[i][j][e] = out[i][j][e] + v;
       }
-      *(half8*)&s.b[r][e0 + 8 * c] = lo;
-      *(half8*)&s.b[r][e0 + 32 + 8 * c] = hi;
+      acc0[i][j] = floatx16{};
+      acc1[i][j] = floatx16{};
     }
-    if constexpr (MODE == GEMM_Q8K) {
-      // mins of sub-blocks 2g, 2g + 1, each for its two 16-element halves (16-sums 8g .. 8g+3)
-      s.b16[r][4 * g] = (_Float16)m0;
-      s.b16[r][4 * g + 1] = (_Float16)m0;
-      s.b16[r][4 * g + 2] = (_Float16)m1;
-      s.b16[r][4 * g + 3] = (_Float16)m1;
-    }
-  }
-  if constexpr (MODE == GEMM_Q8K) {
-    if (hf == 0) {
-      s.dw[r] = d;
-      s.dm[r] = dmin;
-    }
-  }
 }
 
 template <int MODE>
 __global__ void __launch_bounds__(GT, 1) gemm_q4k_kernel(const GemmArgs g) {
   __shared__ GemmSmem s;
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int wm = wid >> 1, wn = wid & 1;  // wave tile: rows 64 wm .., cols 64 wn ..
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   const int nkb = g.K / 256;
-  const int lr = lane & 31, lk = 8 * (lane >> 5);  // MFMA operand lane mapping
+  const int lr = lane & 31;
 
-  floatx16 out[2][2];
-  floatx16 acc0[2][2], acc1[2][2], accm[2][2];
+  floatx16 out[2][2], acc0[2][2], acc1[2][2];
 #pragma unroll
   for (int i = 0; i < 2; i++)
 #pragma unroll
@@ -193,64 +252,34 @@ __global__ void __launch_bounds__(GT, 1) gemm_q4k_kernel(const GemmArgs g) {
       out[i][j] = floatx16{};
       acc0[i][j] = floatx16{};
       acc1[i][j] = floatx16{};
-      accm[i][j] = floatx16{};
     }
 
-  Stage<MODE> st;
-  stage_load<MODE>(g, m0, n0, 0, st);
+  // prologue: step 0 in LDS, step 1 in registers
+  Stage st;
+  stage_load<MODE, 0>(g, m0, n0, 0, st);
+  stage_store<MODE, 0>(st, s.t[0], s.blk[0]);
+  stage_load<MODE, 1>(g, m0, n0, 0, st);
+  __syncthreads();
   for (int kb = 0; kb < nkb; kb++) {
-    __syncthreads();  // the previous step's MFMAs are done with the LDS tiles
-    stage_store<MODE>(st, s);
+    // past the last block the next block is the last one again (clamped), staged into the tile
+    // and block buffer that are not read again
+    const int kn = kb + 1 < nkb ? kb + 1 : kb;
+    // first half of super-block kb (tile t[0]): stage the second half, fetch the next block's
+    // first half
+    stage_store<MODE, 1>(st, s.t[1], s.blk[kb & 1]);
+    stage_load<MODE, 0>(g, m0, n0, kn, st);
+    if constexpr (MODE == GEMM_Q8K) mfma_step(s.t[0], acc0);
+    else mfma_step(s.t[0], out);
+    interleave_step();
     __syncthreads();
-    // next step's loads in flight during the MFMAs (unconditional: the last step re-reads itself)
-    stage_load<MODE>(g, m0, n0, kb + 1 < nkb ? kb + 1 : kb, st);
-
-#pragma unroll
-    for (int kk = 0; kk < BK; kk += 16) {
-      half8 a[2], b[2];
-#pragma unroll
-      for (int i = 0; i < 2; i++) a[i] = *(const half8*)&s.a[64 * wm + 32 * i + lr][kk + lk];
-#pragma unroll
-      for (int j = 0; j < 2; j++) b[j] = *(const half8*)&s.b[64 * wn + 32 * j + lr][kk + lk];
-#pragma unroll
-      for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-          if constexpr (MODE == GEMM_Q8K) {
-            if (kk < 128) acc0[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc0[i][j], 0, 0, 0);
-            else acc1[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc1[i][j], 0, 0, 0);
-          } else {
-            out[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], out[i][j], 0, 0, 0);
-          }
-        }
-    }
-    if constexpr (MODE == GEMM_Q8K) {
-      half8 a[2], b[2];
-#pragma unroll
-      for (int i = 0; i < 2; i++) a[i] = *(const half8*)&s.a16[64 * wm + 32 * i + lr][lk];
-#pragma unroll
-      for (int j = 0; j < 2; j++) b[j] = *(const half8*)&s.b16[64 * wn + 32 * j + lr][lk];
-#pragma unroll
-      for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-          accm[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], floatx16{}, 0, 0, 0);
-          // per block, candle's f32 arithmetic: y += (d_w d_x) isum - (dmin_w d_x) msum
-          const int col = 64 * wn + 32 * j + lr;
-          const float dw = s.dw[col], dm = s.dm[col];
-#pragma unroll
-          for (int e = 0; e < 16; e++) {
-            const int row = 64 * wm + 32 * i + (e / 4) * 8 + (lane >> 5) * 4 + (e % 4);
-            const float dx = s.dx[row];
-            const float isum = acc0[i][j][e] + acc1[i][j][e];
-            const float dd = dw * dx, ddm = dm * dx;
-            const float v = dd * isum - ddm * accm[i][j][e];
-            out[i][j][e] = out[i][j][e] + v;
-          }
-          acc0[i][j] = floatx16{};
-          acc1[i][j] = floatx16{};
-        }
-    }
+    // second half (tile t[1]): stage the next block's first half, fetch its second half
+    stage_store<MODE, 0>(st, s.t[0], s.blk[(kb + 1) & 1]);
+    stage_load<MODE, 1>(g, m0, n0, kn, st);
+    if constexpr (MODE == GEMM_Q8K) mfma_step(s.t[1], acc1);
+    else mfma_step(s.t[1], out);
+    interleave_step();
+    if constexpr (MODE == GEMM_Q8K) block_end(s.blk[kb & 1], acc0, acc1, out);
+    __syncthreads();
   }
 
   // epilogue: y[m][n] = out (+ resid[m][n])
@@ -317,11 +346,14 @@ __global__ void __launch_bounds__(256) act_prep_kernel(const ActPrepArgs a) {
       v.w = v.w / rms * w.w;
     }
     const float e[4] = {v.x, v.y, v.z, v.w};
-    if (a.mode == GEMM_Q8K) {
+    if (a.mode == GEMM_Q8K) {  // the int8 values, stored as (exact) fp16 for the MFMA operand
       int qsum;
       float d;
       const int packed = q8k_block_wave(e, &qsum, &d);
-      ((int*)(a.aq + (size_t)m * K + (size_t)b * 256))[lane] = packed;
+      uint2 h;
+      h.x = (uint32_t)f2h((float)(int8_t)(packed & 0xff)) | ((uint32_t)f2h((float)(int8_t)((packed >> 8) & 0xff)) << 16);
+      h.y = (uint32_t)f2h((float)(int8_t)((packed >> 16) & 0xff)) | ((uint32_t)f2h((float)(int8_t)(packed >> 24)) << 16);
+      ((uint2*)(a.af + (size_t)m * K + (size_t)b * 256))[lane] = h;
       if ((lane & 3) == 0) a.as16[(size_t)m * (K / 16) + b * 16 + (lane >> 2)] = (int16_t)qsum;
       if (lane == 0) a.ad[(size_t)m * nb + b] = d;
     } else {
@@ -338,7 +370,7 @@ __global__ void __launch_bounds__(256) act_prep_kernel(const ActPrepArgs a) {
 int launch_act_prep(const ActPrepArgs& a, hipStream_t s) {
   if (a.M <= 0 || a.K <= 0 || a.K % 256 || a.ldx < a.K || a.ldx % 4) return fail(TPT_ERR_INVALID, "act_prep: bad shape");
   if (!a.x) return fail(TPT_ERR_INVALID, "act_prep: null input");
-  if (a.mode == GEMM_Q8K ? (!a.aq || !a.ad || !a.as16) : !a.af) return fail(TPT_ERR_INVALID, "act_prep: null output");
+  if (!a.af || (a.mode == GEMM_Q8K && (!a.ad || !a.as16))) return fail(TPT_ERR_INVALID, "act_prep: null output");
   hipLaunchKernelGGL(act_prep_kernel, dim3((unsigned)a.M), dim3(256), 0, s, a);
   TPT_HIP(hipGetLastError());
   return TPT_OK;
@@ -349,8 +381,8 @@ int launch_gemm_q4k(const GemmArgs& g, hipStream_t s) { return launch_gemm_q4k_t
 int launch_gemm_q4k_timed(const GemmArgs& g, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.K % 256) return fail(TPT_ERR_INVALID, "gemm: K must be a positive multiple of 256, M and N positive");
   if (!g.w || !g.y) return fail(TPT_ERR_INVALID, "gemm: null weight/output pointer");
-  if (g.mode == GEMM_Q8K && (!g.aq || !g.ad || !g.as16)) return fail(TPT_ERR_INVALID, "gemm: Q8_K mode needs q, d and per-16 sums");
-  if (g.mode == GEMM_F16 && !g.af) return fail(TPT_ERR_INVALID, "gemm: F16 mode needs fp16 activations");
+  if (!g.af) return fail(TPT_ERR_INVALID, "gemm: null activation rows");
+  if (g.mode == GEMM_Q8K && (!g.ad || !g.as16)) return fail(TPT_ERR_INVALID, "gemm: Q8_K mode needs d and per-16 sums");
   if ((g.w_stride % 16) || ((uintptr_t)g.w % 16)) return fail(TPT_ERR_INVALID, "gemm: weight rows must be 16-byte aligned");
   const dim3 grid((unsigned)((g.N + BN - 1) / BN), (unsigned)((g.M + BM - 1) / BM));
   if (g.mode == GEMM_Q8K) hipExtLaunchKernelGGL(gemm_q4k_kernel<GEMM_Q8K>, grid, dim3(GT), 0, s, ev0, ev1, 0, g);

@@ -63,10 +63,9 @@ struct GemmArgs {
   int M = 0, N = 0, K = 0, mode = GEMM_Q8K;
   const uint8_t* w = nullptr;
   size_t w_stride = 0;               // bytes per weight row
-  const int8_t* aq = nullptr;        // GEMM_Q8K: [M][K] int8
-  const float* ad = nullptr;         //           [M][K/256] block scales
+  const uint16_t* af = nullptr;      // [M][K] fp16 bits (GEMM_Q8K: the Q8_K int8 values, exact)
+  const float* ad = nullptr;         // GEMM_Q8K: [M][K/256] block scales
   const int16_t* as16 = nullptr;     //           [M][K/16] per-16 sums
-  const uint16_t* af = nullptr;      // GEMM_F16: [M][K] fp16 bits
   float* y = nullptr;
   int ldy = 0;
   const float* resid = nullptr;      // optional: y = X.W^T + resid
@@ -77,7 +76,8 @@ int launch_gemm_q4k(const GemmArgs& g, hipStream_t s);
 int launch_gemm_q4k_timed(const GemmArgs& g, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1);
 
 // Activation rows for the prefill GEMM: optional RMSNorm (w, eps) or SwiGLU (silu(x) * x2),
-// then Q8_K quantization (aq/ad/as16) or fp16 conversion (af).  x rows of K floats, stride ldx.
+// then Q8_K quantization (the int8 values as fp16 in af, with ad/as16) or fp16 conversion (af).
+// x rows of K floats, stride ldx.
 struct ActPrepArgs {
   int M = 0, K = 0, ldx = 0;
   const float* x = nullptr;
@@ -85,7 +85,6 @@ struct ActPrepArgs {
   const float* norm_w = nullptr;     // RMSNorm weights (nullptr: no norm)
   float eps = 0.f;
   int mode = GEMM_Q8K;
-  int8_t* aq = nullptr;
   float* ad = nullptr;
   int16_t* as16 = nullptr;
   uint16_t* af = nullptr;

@@ -613,7 +613,7 @@ int tpt_model::prefill_scratch(int T, int n_chunks) {
   const int F = desc.ffn, Kmax = std::max(std::max(H, qd), F);
   size_t off = 0;
   auto carve = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes, 256); return o; };
-  const size_t o_x = carve((size_t)T * H * 4), o_aq = carve((size_t)T * Kmax),
+  const size_t o_x = carve((size_t)T * H * 4), o_af = carve((size_t)T * Kmax * 2),
                o_ad = carve((size_t)T * (Kmax / 256) * 4), o_as = carve((size_t)T * (Kmax / 16) * 2),
                o_qkv = carve((size_t)T * (qd + 2 * kd) * 4), o_q = carve((size_t)T * qd * 4),
                o_att = carve((size_t)T * qd * 4), o_g = carve((size_t)T * F * 4), o_u = carve((size_t)T * F * 4),
@@ -631,7 +631,7 @@ int tpt_model::prefill_scratch(int T, int n_chunks) {
   }
   uint8_t* b = (uint8_t*)pf_mem;
   pf_x = (float*)(b + o_x);
-  pf_aq = (int8_t*)(b + o_aq);
+  pf_af = (uint16_t*)(b + o_af);
   pf_ad = (float*)(b + o_ad);
   pf_as16 = (int16_t*)(b + o_as);
   pf_qkv = (float*)(b + o_qkv);
@@ -677,14 +677,14 @@ int tpt_model::batched_layers(int T, int p0, int l0, int l1) {
   auto prep = [&](const float* xx, const float* x2, int K, const float* nw) {
     ActPrepArgs a;
     a.M = T; a.K = K; a.ldx = K; a.x = xx; a.x2 = x2; a.norm_w = nw; a.eps = desc.rms_eps;
-    a.mode = GEMM_Q8K; a.aq = pf_aq; a.ad = pf_ad; a.as16 = pf_as16;
+    a.mode = GEMM_Q8K; a.af = pf_af; a.ad = pf_ad; a.as16 = pf_as16;
     return launch_act_prep(a, stream);
   };
   auto gemm = [&](const uint8_t* w, int K, int N, float* y, int ldy, const float* resid) {
     GemmArgs g;
     g.M = T; g.N = N; g.K = K; g.mode = GEMM_Q8K;
     g.w = w; g.w_stride = row_bytes(TPT_TYPE_Q4_K, K);
-    g.aq = pf_aq; g.ad = pf_ad; g.as16 = pf_as16;
+    g.af = pf_af; g.ad = pf_ad; g.as16 = pf_as16;
     g.y = y; g.ldy = ldy; g.resid = resid; g.ldr = ldy;
     return launch_gemm_q4k(g, stream);
   };

@@ -68,7 +68,7 @@ struct tpt_model {
   size_t pf_bytes = 0;
   float *pf_x = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_att = nullptr, *pf_g = nullptr,
         *pf_u = nullptr, *pf_part = nullptr, *pf_ad = nullptr;
-  int8_t* pf_aq = nullptr;
+  uint16_t* pf_af = nullptr;  // activation rows for the GEMMs (fp16)
   int16_t* pf_as16 = nullptr;
   uint32_t* pf_ids = nullptr;
 
