@@ -116,25 +116,49 @@ __device__ __forceinline__ void stage_store(const Stage& st, GemmTile& T, GemmBl
   get_scale_min(st.h, 2 * g + 1, &sc1, &m1);
   const uint32_t w[8] = {st.q[0].x, st.q[0].y, st.q[0].z, st.q[0].w, st.q[1].x, st.q[1].y, st.q[1].z, st.q[1].w};
   const int e0 = 64 * hf;
+  if constexpr (MODE == GEMM_Q8K) {
+    // the integers sc * q two at a time in packed fp16, all exact: a byte pair (b, b') moved to
+    // the two halves, its nibbles ORed into the mantissa of 1024.0 (0x6400) give 1024 + q,
+    // minus 1024 gives q, times sc gives sc * q <= 945 < 2048
+    typedef _Float16 half2 __attribute__((ext_vector_type(2)));
+    const half2 s0 = {(_Float16)sc0, (_Float16)sc0}, s1 = {(_Float16)sc1, (_Float16)sc1};
+    const half2 k1024 = {(_Float16)1024.f, (_Float16)1024.f};
+    auto dec = [&](uint32_t pair, half2 sc) {
+      const half2 v = __builtin_bit_cast(half2, (pair & 0x000F000Fu) | 0x64006400u) - k1024;
+      return __builtin_bit_cast(uint32_t, v * sc);
+    };
 #pragma unroll
-  for (int c = 0; c < 4; c++) {  // 8 consecutive elements per half8 store
-    half8 lo, hi;
+    for (int c = 0; c < 4; c++) {  // 8 consecutive elements per 16-byte store
+      u32x4 lo, hi;
 #pragma unroll
-    for (int t = 0; t < 8; t++) {
-      const uint32_t byte = (w[2 * c + t / 4] >> (8 * (t % 4))) & 0xff;
-      const int ql = byte & 0xF, qh = byte >> 4;
-      if constexpr (MODE == GEMM_Q8K) {
-        lo[t] = (_Float16)(sc0 * ql);
-        hi[t] = (_Float16)(sc1 * qh);
-      } else {
+      for (int h = 0; h < 2; h++) {
+        const uint32_t x = w[2 * c + h];
+        const uint32_t p01 = __builtin_amdgcn_perm(0u, x, 0x0c010c00u);  // bytes 0, 1 -> halves
+        const uint32_t p23 = __builtin_amdgcn_perm(0u, x, 0x0c030c02u);  // bytes 2, 3 -> halves
+        lo[2 * h] = dec(p01, s0);
+        lo[2 * h + 1] = dec(p23, s0);
+        hi[2 * h] = dec(p01 >> 4, s1);
+        hi[2 * h + 1] = dec(p23 >> 4, s1);
+      }
+      *(u32x4*)&T.b[r][e0 + 8 * c] = lo;
+      *(u32x4*)&T.b[r][e0 + 32 + 8 * c] = hi;
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < 4; c++) {  // 8 consecutive elements per half8 store
+      half8 lo, hi;
+#pragma unroll
+      for (int t = 0; t < 8; t++) {
+        const uint32_t byte = (w[2 * c + t / 4] >> (8 * (t % 4))) & 0xff;
+        const int ql = byte & 0xF, qh = byte >> 4;
         const float d1 = d * (float)sc0, mm1 = dmin * (float)m0;
         const float d2 = d * (float)sc1, mm2 = dmin * (float)m1;
         lo[t] = (_Float16)(d1 * (float)ql - mm1);
         hi[t] = (_Float16)(d2 * (float)qh - mm2);
       }
+      *(half8*)&T.b[r][e0 + 8 * c] = lo;
+      *(half8*)&T.b[r][e0 + 32 + 8 * c] = hi;
     }
-    *(half8*)&T.b[r][e0 + 8 * c] = lo;
-    *(half8*)&T.b[r][e0 + 32 + 8 * c] = hi;
   }
   if constexpr (MODE == GEMM_Q8K) {
     // mins of sub-blocks 2g, 2g + 1, each for its two 16-element halves (16-sums 8g .. 8g+3)
