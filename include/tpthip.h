@@ -117,6 +117,17 @@ int tpt_attn_decode(tpt_ctx* ctx, const float* q, const void* k_cache, const voi
                     int kv_type, float* o, int nq, int nkv, int hd, int L, int L_stride,
                     int n_chunks);
 
+/* Causal attention of a prompt batch: T query rows q [T][Nq*hd], row t at position L0 + t seeing
+ * cache positions [0, L0 + t] (the cache must hold positions < L0 + T); o [T][Nq*hd].  The
+ * attention of candle's batched prompt forward (candle_engine.rs:272-273: the whole prompt in one
+ * quantized_llama forward under its causal mask); the reference's wgpu engine runs
+ * attention.wgsl:31-170 once per position instead.  form 0: the model's choice (matrix cores
+ * where supported: fp16 cache, hd 64 or 128, Nq/Nkv 1, 2, 4 or 8; else per-query split-K),
+ * 1: per-query split-K, 2: matrix cores (TPT_ERR_UNSUPPORTED outside their shapes). */
+int tpt_attn_prefill(tpt_ctx* ctx, const float* q, const void* k_cache, const void* v_cache,
+                     int kv_type, float* o, int nq, int nkv, int hd, int L0, int T, int L_stride,
+                     int form);
+
 /* Greedy token of a logits vector: the last index among equal maxima under f32 total order
  * (candle LogitsProcessor::sample_argmax, used by sample_token wgpu_engine.rs:868-878). */
 int tpt_argmax(tpt_ctx* ctx, const float* logits, int64_t n, uint32_t* out_host);

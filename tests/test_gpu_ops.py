@@ -230,6 +230,95 @@ def test_attention_chunking_invariant(ctx, n_chunks):
     assert rel_l2(o, ref) < 1e-5
 
 
+# ---------------------------------------------------------------- causal (prompt) attention
+
+def causal_case(ctx, nq, nkv, hd, L0, T, seed, form, qmag=1.0, kv_dtype=np.float16):
+    """T query rows at positions L0 .. L0+T-1 over a cache holding positions < L0 + T; the
+    cache rows past that hold NaN, which no query may read.  Returns (gpu, oracle): the oracle
+    is its single-position attention over the first L0 + t + 1 positions, row by row."""
+    rng = np.random.default_rng(seed)
+    stride = L0 + T + 40
+    k = rng.standard_normal((nkv, stride, hd)).astype(kv_dtype)
+    v = rng.standard_normal((nkv, stride, hd)).astype(kv_dtype)
+    k[:, L0 + T:] = np.nan
+    v[:, L0 + T:] = np.nan
+    q = (rng.standard_normal((T, nq * hd)) * qmag).astype(np.float32)
+    kvt = tpthip.TYPE_F32 if kv_dtype == np.float32 else tpthip.TYPE_F16
+    o = ctx.attn_prefill(ctx.to_device(q), ctx.to_device(k), ctx.to_device(v), nq, nkv, hd, L0, T,
+                         stride, form=form, kv_type=kvt)
+    kf, vf = k.astype(np.float32), v.astype(np.float32)
+    ref = np.stack([oracle.attention(q[t], kf, vf, nq, nkv, hd, L0 + t + 1) for t in range(T)])
+    return o, ref
+
+
+CAUSAL_SHAPES = [
+    (32, 8, 128, 0, 256),    # Llama-3 8B heads, a prompt from position 0
+    (32, 8, 128, 1000, 77),  # a ragged batch after a cached prefix
+    (32, 8, 64, 5, 200),     # 1B heads, first position not on a 32-key block
+    (4, 2, 64, 0, 150),      # the tiny test model's heads
+    (16, 16, 128, 31, 33),   # MHA, the diagonal across two key blocks
+    (16, 2, 64, 0, 1),       # one query
+    (64, 8, 128, 3, 45),     # 8 query heads per kv head
+]
+
+
+@pytest.mark.parametrize("form", ["splitk", "mfma"])
+@pytest.mark.parametrize("nq,nkv,hd,L0,T", CAUSAL_SHAPES)
+def test_causal_attention_matches_oracle(ctx, nq, nkv, hd, L0, T, form):
+    """Both causal forms against the oracle: the per-query split-K kernel and the matrix-core
+    flash kernel (fp16 pairs for q and p, 2^-20 relative per operand)."""
+    f = ctx.ATTN_SPLITK if form == "splitk" else ctx.ATTN_MFMA
+    o, ref = causal_case(ctx, nq, nkv, hd, L0, T, seed=T + L0 + hd, form=f)
+    assert np.isfinite(o).all()
+    assert rel_l2(o, ref) < 1e-5
+    # peaked softmax (scores of a few units): the log2-domain running max must track it
+    o, ref = causal_case(ctx, nq, nkv, hd, L0, T, seed=T + L0 + hd + 1, form=f, qmag=6.0)
+    assert rel_l2(o, ref) < 1e-5
+
+
+def test_causal_forms_agree_prompt_shape(ctx):
+    """The 8B prompt slice of the batched prefill (1024 queries after 1024 cached positions):
+    the two causal forms agree to f32 accuracy at full size."""
+    nq, nkv, hd, L0, T = 32, 8, 128, 1024, 1024
+    rng = np.random.default_rng(77)
+    k = ctx.to_device(rng.standard_normal((nkv, L0 + T, hd)).astype(np.float16))
+    v = ctx.to_device(rng.standard_normal((nkv, L0 + T, hd)).astype(np.float16))
+    q = ctx.to_device((rng.standard_normal((T, nq * hd)) * 2).astype(np.float32))
+    a = ctx.attn_prefill(q, k, v, nq, nkv, hd, L0, T, L0 + T, form=ctx.ATTN_SPLITK)
+    b = ctx.attn_prefill(q, k, v, nq, nkv, hd, L0, T, L0 + T, form=ctx.ATTN_MFMA)
+    assert rel_l2(b, a) < 1e-5
+
+
+def test_causal_attention_closed_forms(ctx):
+    """Query 0 at position 0 sees one key: o = v_0 exactly; identical K rows give uniform
+    weights: o = mean of V over the visible positions."""
+    nq, nkv, hd = 8, 2, 128
+    rng = np.random.default_rng(9)
+    q = rng.standard_normal((40, nq * hd)).astype(np.float32)
+    k = np.repeat(rng.standard_normal((nkv, 1, hd)).astype(np.float16), 64, axis=1)
+    v = rng.standard_normal((nkv, 64, hd)).astype(np.float16)
+    o = ctx.attn_prefill(ctx.to_device(q), ctx.to_device(k), ctx.to_device(v), nq, nkv, hd, 0, 40,
+                         64, form=ctx.ATTN_MFMA)
+    g = nq // nkv
+    np.testing.assert_array_equal(o[0], np.repeat(v[:, 0, :].astype(np.float32), g, axis=0).reshape(-1))
+    for t in (1, 31, 32, 39):
+        want = np.repeat(v[:, :t + 1, :].astype(np.float64).mean(axis=1), g, axis=0).reshape(-1)
+        assert rel_l2(o[t], want) < 1e-6, t
+
+
+def test_causal_mfma_unsupported_shapes(ctx):
+    """hd 96 and the f32 cache stay on the split-K form; asking the matrix cores for them fails."""
+    for hd, dt in ((96, np.float16), (128, np.float32)):
+        q = ctx.to_device(np.zeros((4, 8 * hd), np.float32))
+        kv = ctx.to_device(np.zeros((2, 8, hd), dt))
+        kvt = tpthip.TYPE_F32 if dt == np.float32 else tpthip.TYPE_F16
+        with pytest.raises(tpthip.TptError) as e:
+            ctx.attn_prefill(q, kv, kv, 8, 2, hd, 0, 4, 8, form=ctx.ATTN_MFMA, kv_type=kvt)
+        assert e.value.code == tpthip.ERR_UNSUPPORTED
+        o = ctx.attn_prefill(q, kv, kv, 8, 2, hd, 0, 4, 8, kv_type=kvt)  # auto: split-K
+        assert np.all(o == 0)
+
+
 def test_argmax_semantics(ctx):
     cases = [
         (np.array([1, 3, 3, 2], np.float32), 2),

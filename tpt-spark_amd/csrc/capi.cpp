@@ -229,6 +229,31 @@ int tpt_attn_decode(tpt_ctx* c, const float* q, const void* k_cache, const void*
   return rc;
 }
 
+int tpt_attn_prefill(tpt_ctx* c, const float* q, const void* k_cache, const void* v_cache,
+                     int kv_type, float* o, int nq, int nkv, int hd, int L0, int T, int L_stride,
+                     int form) {
+  ENTER(c);
+  if (T <= 0 || L0 < 0 || form < 0 || form > 2) return fail(TPT_ERR_INVALID, "attn_prefill: bad T, L0 or form");
+  if ((long)L0 + T > L_stride) return fail(TPT_ERR_INVALID, "attn_prefill: queries past the cache");
+  // the split-K partition is sized for the last query, which sees L0 + T positions
+  AttnCall call;
+  int rc = attn_prepare(c, q, k_cache, v_cache, kv_type, o, nq, nkv, hd, L0 + T, L_stride, 0, &call);
+  if (rc) return rc;
+  (void)hipFreeAsync(call.scratch, c->stream);
+  call.scratch = nullptr;
+  AttnArgs& a = call.a;
+  a.L_host = L0 + 1;
+  a.nqb = T;
+  a.ldq = a.ldo = nq * hd;
+  const bool mfma = form == 2 || (form == 0 && attn_causal_mfma_supported(a));
+  if (mfma) return launch_attn_causal_mfma(a, c->stream);
+  TPT_HIP(hipMallocAsync(&call.scratch, (size_t)T * attn_part_floats(nq, nkv, hd, a.n_chunks) * 4, c->stream));
+  a.part = (float*)call.scratch;
+  rc = launch_attn_decode(a, c->stream);
+  (void)hipFreeAsync(call.scratch, c->stream);
+  return rc;
+}
+
 int tpt_bench_attn(tpt_ctx* c, const float* q, const void* const* k_caches,
                    const void* const* v_caches, int n_caches, int kv_type, float* o, int nq,
                    int nkv, int hd, int L, int L_stride, int n_chunks, int iters, float* ms_out) {

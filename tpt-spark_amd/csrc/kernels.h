@@ -121,6 +121,11 @@ int attn_default_chunks(int L, int nkv);
 int attn_chunk_len(int L, int n_chunks);  // smallest multiple of 16 covering L in n_chunks
 int attn_max_len();  // longest cache the split-K partition supports
 int launch_attn_decode(const AttnArgs& a, hipStream_t s);
+// Causal multi-query attention of a prompt batch on the matrix cores (k_attn_causal.hip): query t
+// of nqb sits at position L_host - 1 + t and sees positions [0, L_host + t); fp16 cache, head_dim
+// 64 or 128, Nq/Nkv 1, 2, 4 or 8, 16-byte aligned rows; the chunk fields and part are unused.
+bool attn_causal_mfma_supported(const AttnArgs& a);
+int launch_attn_causal_mfma(const AttnArgs& a, hipStream_t s);
 
 // Start of a decode step: pick the token, embed it (x = dequant(token_embd[tok])), advance the
 // step state and clear the amax slot the LM head will write.

@@ -297,6 +297,8 @@ int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_t
       if (t != TPT_TYPE_Q4_K) batched_prefill = false;
   const char* ev_pf = getenv("TPT_HIP_PREFILL");
   if (ev_pf && strcmp(ev_pf, "steps") == 0) batched_prefill = false;
+  const char* ev_att = getenv("TPT_HIP_CAUSAL_ATTN");
+  causal_mfma = !(ev_att && strcmp(ev_att, "splitk") == 0);
   const char* ev_graph = getenv("TPT_HIP_GRAPHS");
   use_graphs = !(ev_graph && ev_graph[0] == '0');
   if ((rc = setup_decode_layers())) return rc;
@@ -710,7 +712,9 @@ int tpt_model::batched_layers(int T, int p0, int l0, int l1) {
     at.q = pf_q; at.ldq = qd; at.kc = kc; at.vc = vc; at.kv_type = desc.kv_type;
     at.o = pf_att; at.ldo = qd; at.nq = nq; at.nkv = nkv; at.hd = hd; at.L_stride = mc;
     at.L_host = p0 + 1; at.nqb = T; at.n_chunks = nch; at.chunk_len = cl; at.part = pf_part;
-    if ((rc = launch_attn_decode(at, stream))) return rc;
+    rc = causal_mfma && attn_causal_mfma_supported(at) ? launch_attn_causal_mfma(at, stream)
+                                                       : launch_attn_decode(at, stream);
+    if (rc) return rc;
     if ((rc = prep(pf_att, nullptr, qd, nullptr)) || (rc = gemm(L.o, qd, H, pf_x, H, pf_x))) return rc;
     if ((rc = prep(pf_x, nullptr, H, L.ffn_norm)) || (rc = gemm(L.gate, H, F, pf_g, F, nullptr)) ||
         (rc = gemm(L.up, H, F, pf_u, F, nullptr)))

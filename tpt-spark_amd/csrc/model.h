@@ -64,6 +64,7 @@ struct tpt_model {
   // batched prefill (MFMA GEMMs over up to kPrefillT positions at once)
   static constexpr int kPrefillT = 1024;
   bool batched_prefill = false;       // every layer matrix is Q4_K
+  bool causal_mfma = true;            // prompt attention on the matrix cores where supported
   void* pf_mem = nullptr;             // scratch of the batched prefill, grown on demand
   size_t pf_bytes = 0;
   float *pf_x = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_att = nullptr, *pf_g = nullptr,

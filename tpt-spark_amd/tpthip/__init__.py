@@ -102,6 +102,7 @@ EXPORTS = {
     "tpt_engine_reset_cache": ([P], I32),
     "tpt_common_prefix_len": ([P, SZ, P, SZ], SZ),
     "tpt_bench_gemv": ([P, I32, P, I32, P, P, I32, I32, I32, P], I32),
+    "tpt_attn_prefill": ([P, P, P, P, I32, P, I32, I32, I32, I32, I32, I32, I32], I32),
     "tpt_bench_attn": ([P, P, P, P, I32, I32, P, I32, I32, I32, I32, I32, I32, I32, P], I32),
     "tpt_bench_copy": ([P, P, P, SZ, I32, P], I32),
     "tpt_gemm": ([P, I32, P, P, P, I32, I32, I32, I32], I32),
@@ -264,6 +265,16 @@ class Context:
         check(lib().tpt_attn_decode(self.h, qbuf.ptr, kbuf.ptr, vbuf.ptr, kv_type, o.ptr, nq, nkv,
                                     hd, L, L_stride, n_chunks))
         return o.download(np.float32, nq * hd)
+
+    ATTN_AUTO, ATTN_SPLITK, ATTN_MFMA = 0, 1, 2
+
+    def attn_prefill(self, qbuf, kbuf, vbuf, nq, nkv, hd, L0, T, L_stride, form=0,
+                     kv_type=TYPE_F16):
+        """Causal attention of T query rows (row t at position L0 + t); returns o [T, nq*hd]."""
+        o = self.alloc(T * nq * hd * 4)
+        check(lib().tpt_attn_prefill(self.h, qbuf.ptr, kbuf.ptr, vbuf.ptr, kv_type, o.ptr, nq, nkv,
+                                     hd, L0, T, L_stride, form))
+        return o.download(np.float32, T * nq * hd).reshape(T, nq * hd)
 
     def bench_attn(self, qbuf, kbufs, vbufs, obuf, nq, nkv, hd, L, L_stride, iters, n_chunks=0,
                    kv_type=TYPE_F16):
