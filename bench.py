@@ -18,8 +18,9 @@ context's stream, over back-to-back launches that rotate through distinct weight
 K*N*144/256 + 4K + 4N.  traffic comes from the committed rocprofv3 PMC summary when present.
 
 Further legs reported in `config` (not the headline): decode attention at the long-context
-shapes (`attn_decode_f16`, GB/s vs HBM peak over rotating caches) and the MFMA prefill GEMM at the
-prompt shapes (`prefill_gemm_q4k`, TFLOP/s vs the 2.5 PFLOP/s dense fp16 peak).
+shapes (`attn_decode_f16`, GB/s vs HBM peak over rotating caches), the MFMA prefill GEMM at the
+prompt shapes (`prefill_gemm_q4k`, TFLOP/s vs the 2.5 PFLOP/s dense fp16 peak) and the
+matrix-core causal prompt attention (`prefill_attn_causal_f16`, algorithmic TFLOP/s, same peak).
 
 cpu_baseline: the CPU oracle's restatement of candle's CPU decode (Q8_K activation quant,
 integer vec_dot, OpenMP over output columns) timed on this host's cores on a bounded sample of
@@ -117,6 +118,38 @@ def attn_roofline(tp, ctx, iters=64):
     return out
 
 
+# causal prompt attention: (Nq, Nkv, hd, L0 cached positions, T queries) -- the two 1024-query
+# slices of the 2048-token prompt at the Llama-3 8B head shape
+ATTN_CAUSAL_CASES = [(32, 8, 128, 0, 1024), (32, 8, 128, 1024, 1024)]
+
+
+def attn_causal_roofline(tp, ctx, iters=20):
+    """Event-timed matrix-core causal attention at ATTN_CAUSAL_CASES.  Algorithmic flops per
+    launch = 4 * Nq * hd * (visible positions summed over the T queries) -- q.k and p.v, 2 flops
+    per multiply-add; the kernel issues twice that on the matrix cores (fp16 hi/lo operand pairs)
+    plus the masked halves of the diagonal blocks.  Priced against the dense fp16 MFMA peak."""
+    out = {}
+    rng = np.random.default_rng(11)
+    for nq, nkv, hd, L0, T in ATTN_CAUSAL_CASES:
+        L = L0 + T
+        k = ctx.to_device(rng.standard_normal((nkv, L, hd), dtype=np.float32).astype(np.float16))
+        v = ctx.to_device(rng.standard_normal((nkv, L, hd), dtype=np.float32).astype(np.float16))
+        q = ctx.to_device(rng.standard_normal((T, nq * hd), dtype=np.float32))
+        o = ctx.alloc(T * nq * hd * 4)
+        ctx.bench_attn_prefill(q, k, v, o, nq, nkv, hd, L0, T, L, 2)
+        ms = ctx.bench_attn_prefill(q, k, v, o, nq, nkv, hd, L0, T, L, iters)
+        us = ms * 1e3 / iters
+        flops = 4.0 * nq * hd * (T * L0 + T * (T + 1) / 2)
+        tf = flops / (us * 1e-6) / 1e12
+        out[f"{nq}/{nkv}x{hd} L0={L0} T={T}"] = {"flops": flops, "us_per_launch": round(us, 2),
+                                                 "tflops": round(tf, 1),
+                                                 "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}
+        log(f"causal attention {nq}/{nkv} hd {hd} L0 {L0} T {T}: {us:.1f} us/launch, {tf:.1f} TFLOP/s")
+        for b in (k, v, q, o):
+            b.free()
+    return out
+
+
 # prefill GEMM shapes: M prompt rows, K = 4096, N = 4096 (Q/O) and 14336 (gate/up)
 GEMM_CASES = [(M, 4096, N) for M in (128, 512, 2048) for N in (4096, 14336)]
 MFMA_F16_PEAK_TFLOPS = 2500.0
@@ -194,9 +227,10 @@ def main():
     ap.add_argument("--prompt", type=int, default=PROMPT_LEN)
     ap.add_argument("--model", default="", help="existing GGUF (default: generate the 8B shape)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--leg", choices=["all", "gemv", "attn", "gemm"], default="all",
+    ap.add_argument("--leg", choices=["all", "gemv", "attn", "gemm", "causal"], default="all",
                     help="gemv: only the GEMV roofline leg and the copy calibration (profiling); "
-                         "attn: only the decode-attention leg; gemm: only the prefill GEMM leg")
+                         "attn: only the decode-attention leg; gemm: only the prefill GEMM leg; "
+                         "causal: only the prompt-attention leg")
     ap.add_argument("--gemv-iters", type=int, default=256, help="timed launches per GEMV shape")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -216,12 +250,16 @@ def main():
     if args.leg == "gemm":
         print(json.dumps({"prefill_gemm": gemm_roofline(tp, ctx)}))
         return
+    if args.leg == "causal":
+        print(json.dumps({"prefill_attn": attn_causal_roofline(tp, ctx)}))
+        return
     gemv = gemv_roofline(tp, ctx, iters=args.gemv_iters)
     if args.leg == "gemv":
         print(json.dumps({"gemv": gemv, "copy": copy_calibration(ctx)}))
         return
     attn = attn_roofline(tp, ctx)
     gemm = gemm_roofline(tp, ctx)
+    causal = attn_causal_roofline(tp, ctx)
 
     tmpdir = tempfile.mkdtemp(prefix="tpt_bench_", dir=os.environ.get("TPT_BENCH_DIR") or None)
     path = args.model
@@ -300,6 +338,7 @@ def main():
             "gemv_q4k": gemv,
             "attn_decode_f16": attn,
             "prefill_gemm_q4k": gemm,
+            "prefill_attn_causal_f16": causal,
         },
         "roofline": {
             "bound": "hbm",

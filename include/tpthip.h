@@ -81,7 +81,8 @@ int tpt_dequant(tpt_ctx* ctx, int type, const void* w, float* y, int64_t n);
 int tpt_gemv(tpt_ctx* ctx, int type, const void* w, const float* x, float* y, int K, int N,
              int act_mode);
 
-/* Prefill GEMM on MFMA: Y[M,N] = X[M,K] . W[N,K]^T with W in Q4_K rows, X fp32 rows.
+/* Prefill GEMM on MFMA: Y[M,N] = X[M,K] . W[N,K]^T with W in Q4_K or Q6_K rows (type), X fp32
+ * rows (a real Q4_K_M file holds Q6_K attn_v / ffn_down matrices in some layers).
  * act_mode TPT_ACT_Q8: every X row is quantized to Q8_K as candle's QMatMul does and the
  * products are integer-exact (candle's prefill arithmetic); TPT_ACT_F16: X and the dequantized
  * W in fp16 on the matrix cores, fp32 accumulate.  Replaces the per-position prefill of
@@ -150,6 +151,11 @@ int tpt_bench_gemm(tpt_ctx* ctx, int type, const void* w, const float* x, float*
 int tpt_bench_attn(tpt_ctx* ctx, const float* q, const void* const* k_caches,
                    const void* const* v_caches, int n_caches, int kv_type, float* o, int nq,
                    int nkv, int hd, int L, int L_stride, int n_chunks, int iters, float* ms_out);
+/* iters back-to-back launches of tpt_attn_prefill's matrix-core form over the same caches
+ * (T queries after L0 cached positions); *ms_out = the event time over all launches. */
+int tpt_bench_attn_prefill(tpt_ctx* ctx, const float* q, const void* k_cache, const void* v_cache,
+                           int kv_type, float* o, int nq, int nkv, int hd, int L0, int T,
+                           int L_stride, int iters, float* ms_out);
 /* iters launches of a plain vector copy of `bytes` (HBM calibration for PMC counters) */
 int tpt_bench_copy(tpt_ctx* ctx, void* dst, const void* src, size_t bytes, int iters,
                    float* ms_out);

@@ -310,6 +310,58 @@ def test_tiny_long_prompt_matches_oracle(ctx, tiny_gguf, tiny_oracle, kv):
 
 
 @pytest.fixture(scope="module")
+def mixed_gguf(tmp_path_factory):
+    """The tiny model typed as a real Q4_K_M file is: attn_v and ffn_down Q6_K in the layers
+    llama.cpp's recipe gives more bits (here layer 1), everything else Q4_K."""
+    path = str(tmp_path_factory.mktemp("mixed") / "tiny-q4_k_m-mixed.gguf")
+    synth.write_llama(path, synth.TINY, seed=8, type_more_bits=tpthip.TYPE_Q6_K)
+    return path
+
+
+def test_mixed_q4k_q6k_prefill(ctx, mixed_gguf):
+    """Q6_K layer matrices stay on the batched MFMA prefill (the Q6_K GEMM): the layer holding
+    Q6_K attn_v / ffn_down equals the step path on the same rows, and the 150-token prompt's
+    logits match the oracle (f32 cache, candle's).  The step-by-step prefill is held to the
+    oracle's own spread under a change of its dot-product summation order: over 150 positions a
+    Q8_K activation value can round the other way under an f32 ordering difference (measured:
+    the step path meets the oracle to 1e-7 at 40, 64, 80 and 129 tokens and moves by ~1e-2 at
+    100, 128 and 150), and the random-init model carries such a flip to the logits."""
+    prompt = [int(t) for t in np.random.default_rng(6).integers(0, 1024, 150)]
+    om = oracle.Model(mixed_gguf)
+    try:
+        om.reset(256, kv_f16=False)
+        ref = om.forward(prompt, 0)
+        oracle.set_dot_block_order(True)
+        om.reset(256, kv_f16=False)
+        alt = om.forward(prompt, 0)
+    finally:
+        oracle.set_dot_block_order(False)
+        om.close()
+    spread = float(np.abs(alt - ref).max())
+    m_b = tpthip.Model(ctx, mixed_gguf, max_ctx=256, kv_type=tpthip.TYPE_F32)
+    os.environ["TPT_HIP_PREFILL"] = "steps"
+    try:
+        m_s = tpthip.Model(ctx, mixed_gguf, max_ctx=256, kv_type=tpthip.TYPE_F32)
+    finally:
+        del os.environ["TPT_HIP_PREFILL"]
+    try:
+        rows = np.random.default_rng(2).standard_normal((40, m_b.desc["embed"])).astype(np.float32)
+        yb = m_b.run_layers(rows, 0, 1, 2, path=0)
+        ys = m_s.run_layers(rows, 0, 1, 2, path=1)
+        nb, lb = m_b.prefill(prompt, 0, logits=True)
+        ns, ls = m_s.prefill(prompt, 0, logits=True)
+        print("layer 1 batched vs steps rel-l2", _rel_l2(yb, ys), "| batched vs oracle",
+              np.abs(lb - ref).max(), "| steps vs oracle", np.abs(ls - ref).max(), "| oracle spread", spread)
+        assert _rel_l2(yb, ys) < 1e-4
+        assert nb == oracle.argmax(ref)
+        assert np.abs(lb - ref).max() < 1e-3
+        assert np.abs(ls - ref).max() < 2 * spread + 1e-3
+    finally:
+        m_b.close()
+        m_s.close()
+
+
+@pytest.fixture(scope="module")
 def gguf_1b(tmp_path_factory):
     """Llama 1B shape (16 layers, hidden 2048, 32/8 heads, head_dim 64, FFN 8192, vocab 128256,
     theta 500000), Q4_K_M, weights N(0, 0.02), norms 1."""

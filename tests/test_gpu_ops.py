@@ -335,8 +335,8 @@ def test_argmax_semantics(ctx):
 
 # ---------------------------------------------------------------- prefill GEMM (MFMA)
 
-def gemm_case(ctx, M, K, N, seed, bf16=False):
-    w = synth.random_weights(TYPE_Q4_K, N, K, seed=seed, name=f"g{K}x{N}")
+def gemm_case(ctx, M, K, N, seed, bf16=False, qtype=TYPE_Q4_K):
+    w = synth.random_weights(qtype, N, K, seed=seed, name=f"g{K}x{N}")
     x = np.random.default_rng(seed).standard_normal((M, K)).astype(np.float32)
     if bf16:  # bf16 activations (values exactly representable in bf16)
         x = (x.view(np.uint32) & 0xFFFF0000).view(np.float32)
@@ -345,38 +345,69 @@ def gemm_case(ctx, M, K, N, seed, bf16=False):
 
 @pytest.mark.parametrize("M,K,N", [(16, 256, 64), (33, 512, 300), (128, 4096, 4096), (200, 2048, 1000),
                                    (130, 14336, 256)])
-def test_gemm_q8k_matches_candle(ctx, M, K, N):
+@pytest.mark.parametrize("qtype", [TYPE_Q4_K, TYPE_Q6_K])
+def test_gemm_q8k_matches_candle(ctx, M, K, N, qtype):
     """Q8_K mode: candle's prefill arithmetic (each X row quantized to Q8_K, integer dots);
     the integer sums are exact, so only f32 block accumulation order differs."""
-    w, x = gemm_case(ctx, M, K, N, seed=M + K + N)
-    y = ctx.gemm(TYPE_Q4_K, ctx.to_device(w), ctx.to_device(x), M, K, N, act=tpthip.ACT_Q8)
+    w, x = gemm_case(ctx, M, K, N, seed=M + K + N, qtype=qtype)
+    y = ctx.gemm(qtype, ctx.to_device(w), ctx.to_device(x), M, K, N, act=tpthip.ACT_Q8)
     rows = np.arange(M) if M * N <= 200 * 1000 else np.random.default_rng(0).choice(M, 24, replace=False)
-    ref = oracle.matmul(TYPE_Q4_K, x[rows], w, N)
+    ref = oracle.matmul(qtype, x[rows], w, N)
     for i, r in enumerate(rows):
         assert rel_l2(y[r], ref[i]) < 1e-5, r
 
 
-def test_gemm_q8k_equals_gemv_rows(ctx):
+@pytest.mark.parametrize("qtype", [TYPE_Q4_K, TYPE_Q6_K])
+def test_gemm_q8k_equals_gemv_rows(ctx, qtype):
     """Batched prefill rows equal the decode GEMV of the same row (same Q8_K arithmetic)."""
     M, K, N = 40, 4096, 512
-    w, x = gemm_case(ctx, M, K, N, seed=77)
+    w, x = gemm_case(ctx, M, K, N, seed=77, qtype=qtype)
     wd = ctx.to_device(w)
-    y = ctx.gemm(TYPE_Q4_K, wd, ctx.to_device(x), M, K, N, act=tpthip.ACT_Q8)
+    y = ctx.gemm(qtype, wd, ctx.to_device(x), M, K, N, act=tpthip.ACT_Q8)
     for r in (0, 17, 39):
-        yv = ctx.gemv(TYPE_Q4_K, wd, ctx.to_device(x[r].copy()), K, N)
+        yv = ctx.gemv(qtype, wd, ctx.to_device(x[r].copy()), K, N)
         assert rel_l2(y[r], yv) < 1e-6
 
 
-@pytest.mark.parametrize("M,N", [(128, 4096), (512, 4096), (2048, 4096), (128, 14336), (512, 14336),
-                                 (2048, 14336)])
-def test_gemm_f16_config3(ctx, M, N):
+def q6k_extreme_blocks(n_blocks, seed):
+    """Q6_K blocks whose integers sc * (q - 32) reach the ends of [-4064, 4096] and odd values
+    past 2048 (not representable in fp16): scales from {-128, -127, 127, 65, -1, 0}, every
+    6-bit q, d = 1."""
+    rng = np.random.default_rng(seed)
+    b = np.zeros((n_blocks, 210), np.uint8)
+    b[:, :192] = rng.integers(0, 256, (n_blocks, 192), dtype=np.uint8)  # ql, qh: all q values
+    sc = rng.choice(np.array([-128, -127, 127, 65, -1, 0], np.int8), (n_blocks, 16))
+    b[:, 192:208] = sc.view(np.uint8)
+    b[:, 208:210] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    return b.reshape(-1)
+
+
+def test_gemm_q6k_exact_at_integer_extremes(ctx):
+    """The split w = 64 w1 + w0 keeps every Q6_K product exact where sc * (q - 32) leaves fp16's
+    exact range: rows of +-1 activations (Q8_K values -128 / 127 after quantization) against
+    blocks of extreme scales give the oracle's integers to f32 rounding."""
+    M, K, N = 48, 1024, 64
+    w = q6k_extreme_blocks(N * K // 256, seed=3)
+    x = np.random.default_rng(4).choice(np.array([-1.0, 1.0, 0.5], np.float32), (M, K))
+    y = ctx.gemm(TYPE_Q6_K, ctx.to_device(w), ctx.to_device(x), M, K, N, act=tpthip.ACT_Q8)
+    ref = oracle.matmul(TYPE_Q6_K, x, w, N)
+    assert rel_l2(y, ref) < 1e-6
+    yv = ctx.gemv(TYPE_Q6_K, ctx.to_device(w), ctx.to_device(x[5].copy()), K, N)
+    assert rel_l2(y[5], yv) < 1e-6
+
+
+@pytest.mark.parametrize("M,N,qtype", [(128, 4096, TYPE_Q4_K), (512, 4096, TYPE_Q4_K), (2048, 4096, TYPE_Q4_K),
+                                       (128, 14336, TYPE_Q4_K), (512, 14336, TYPE_Q4_K), (2048, 14336, TYPE_Q4_K),
+                                       (512, 4096, TYPE_Q6_K)])
+def test_gemm_f16_config3(ctx, M, N, qtype):
     """fp16 MFMA mode at the prefill shapes (K=4096, bf16 activations): within 1e-3 relative L2
     of the fp64 product of the exactly dequantized weights (checked on a row/column sample)."""
     K = 4096
-    w, x = gemm_case(ctx, M, K, N, seed=M * 3 + N, bf16=True)
-    y = ctx.gemm(TYPE_Q4_K, ctx.to_device(w), ctx.to_device(x), M, K, N, act=tpthip.ACT_F16)
+    w, x = gemm_case(ctx, M, K, N, seed=M * 3 + N, bf16=True, qtype=qtype)
+    y = ctx.gemm(qtype, ctx.to_device(w), ctx.to_device(x), M, K, N, act=tpthip.ACT_F16)
     nc = min(N, 1024)
-    wdq = oracle.dequant(TYPE_Q4_K, w[: nc * (K // 256) * 144], nc * K).astype(np.float64).reshape(nc, K)
+    rb = (K // 256) * (144 if qtype == TYPE_Q4_K else 210)
+    wdq = oracle.dequant(qtype, w[: nc * rb], nc * K).astype(np.float64).reshape(nc, K)
     rows = np.random.default_rng(1).choice(M, min(M, 64), replace=False)
     ref = x[rows].astype(np.float64) @ wdq.T
     assert rel_l2(y[rows][:, :nc], ref) < 1e-3
@@ -388,4 +419,4 @@ def test_gemm_rejects_bad_shapes(ctx):
     with pytest.raises(tpthip.TptError):
         ctx.gemm(TYPE_Q4_K, w, x, 4, 100, 4, act=tpthip.ACT_Q8)  # K not a multiple of 256
     with pytest.raises(tpthip.TptError):
-        ctx.gemm(TYPE_Q6_K, w, x, 4, 256, 4, act=tpthip.ACT_Q8)  # only Q4_K on the MFMA path
+        ctx.gemm(TYPE_Q8_0, w, x, 4, 256, 4, act=tpthip.ACT_Q8)  # Q4_K and Q6_K on the MFMA path

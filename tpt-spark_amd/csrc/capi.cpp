@@ -254,6 +254,36 @@ int tpt_attn_prefill(tpt_ctx* c, const float* q, const void* k_cache, const void
   return rc;
 }
 
+int tpt_bench_attn_prefill(tpt_ctx* c, const float* q, const void* k_cache, const void* v_cache,
+                           int kv_type, float* o, int nq, int nkv, int hd, int L0, int T,
+                           int L_stride, int iters, float* ms_out) {
+  ENTER(c);
+  if (iters <= 0 || iters > 4096 || !ms_out) return fail(TPT_ERR_INVALID, "bench_attn_prefill: bad arguments");
+  if (!q || !k_cache || !v_cache || !o) return fail(TPT_ERR_INVALID, "bench_attn_prefill: null pointer");
+  if (T <= 0 || L0 < 0 || (long)L0 + T > L_stride || nkv <= 0 || nq % nkv)
+    return fail(TPT_ERR_INVALID, "bench_attn_prefill: bad shape");
+  AttnArgs a;
+  a.q = q; a.kc = k_cache; a.vc = v_cache; a.kv_type = kv_type; a.o = o;
+  a.nq = nq; a.nkv = nkv; a.hd = hd; a.L_stride = L_stride; a.L_host = L0 + 1;
+  a.nqb = T; a.ldq = a.ldo = nq * hd;
+  if (!attn_causal_mfma_supported(a))
+    return fail(TPT_ERR_UNSUPPORTED, "bench_attn_prefill: shape outside the matrix-core kernel");
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  int rc = TPT_OK;
+  hipError_t e = hipEventCreate(&e0);
+  if (e == hipSuccess) e = hipEventCreate(&e1);
+  if (e == hipSuccess) e = hipEventRecord(e0, c->stream);
+  for (int i = 0; i < iters && rc == TPT_OK && e == hipSuccess; i++) rc = launch_attn_causal_mfma(a, c->stream);
+  if (e == hipSuccess) e = hipEventRecord(e1, c->stream);
+  if (e == hipSuccess) e = hipEventSynchronize(e1);
+  if (e == hipSuccess && rc == TPT_OK) e = hipEventElapsedTime(ms_out, e0, e1);
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  if (rc) return rc;
+  if (e != hipSuccess) return hip_fail(e, "bench_attn_prefill", __FILE__, __LINE__);
+  return TPT_OK;
+}
+
 int tpt_bench_attn(tpt_ctx* c, const float* q, const void* const* k_caches,
                    const void* const* v_caches, int n_caches, int kv_type, float* o, int nq,
                    int nkv, int hd, int L, int L_stride, int n_chunks, int iters, float* ms_out) {
@@ -311,12 +341,14 @@ struct GemmCall {
 };
 int gemm_prepare(tpt_ctx* c, int type, const void* w, const float* x, float* y, int M, int K,
                  int N, int act_mode, GemmCall* call) {
-  if (type != TPT_TYPE_Q4_K) return fail(TPT_ERR_UNSUPPORTED, "gemm: weight type must be Q4_K");
+  if (type != TPT_TYPE_Q4_K && type != TPT_TYPE_Q6_K)
+    return fail(TPT_ERR_UNSUPPORTED, "gemm: weight type must be Q4_K or Q6_K");
   if (act_mode != TPT_ACT_Q8 && act_mode != TPT_ACT_F16) return fail(TPT_ERR_INVALID, "gemm: act_mode must be TPT_ACT_Q8 or TPT_ACT_F16");
   if (!w || !x || !y || M <= 0 || N <= 0 || K <= 0 || K % 256) return fail(TPT_ERR_INVALID, "gemm: bad arguments");
   GemmArgs& g = call->g;
   g.M = M; g.N = N; g.K = K;
   g.mode = act_mode == TPT_ACT_Q8 ? GEMM_Q8K : GEMM_F16;
+  g.wtype = type;
   g.w = (const uint8_t*)w;
   g.w_stride = row_bytes(type, K);
   g.y = y;
@@ -349,7 +381,7 @@ int tpt_gemm(tpt_ctx* c, int type, const void* w, const float* x, float* y, int 
   GemmCall call;
   int rc = gemm_prepare(c, type, w, x, y, M, K, N, act_mode, &call);
   if (rc) return rc;
-  rc = launch_gemm_q4k(call.g, c->stream);
+  rc = launch_gemm(call.g, c->stream);
   (void)hipFreeAsync(call.scratch, c->stream);
   return rc;
 }
@@ -366,7 +398,7 @@ int tpt_bench_gemm(tpt_ctx* c, int type, const void* w, const float* x, float* y
   for (auto& v : ev)
     if (e == hipSuccess) e = hipEventCreate(&v);
   for (int i = 0; i < iters && rc == TPT_OK && e == hipSuccess; i++)
-    rc = launch_gemm_q4k_timed(call.g, c->stream, ev[2 * i], ev[2 * i + 1]);
+    rc = launch_gemm_timed(call.g, c->stream, ev[2 * i], ev[2 * i + 1]);
   if (e == hipSuccess && rc == TPT_OK) e = hipEventSynchronize(ev.back());
   float total = 0.f;
   for (int i = 0; i < iters && e == hipSuccess && rc == TPT_OK; i++) {

@@ -294,7 +294,7 @@ int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_t
   batched_prefill = true;
   for (const Layer& L : layers)
     for (int t : {L.tq, L.tk, L.tv, L.to, L.tg, L.tu, L.td})
-      if (t != TPT_TYPE_Q4_K) batched_prefill = false;
+      if (t != TPT_TYPE_Q4_K && t != TPT_TYPE_Q6_K) batched_prefill = false;
   const char* ev_pf = getenv("TPT_HIP_PREFILL");
   if (ev_pf && strcmp(ev_pf, "steps") == 0) batched_prefill = false;
   const char* ev_att = getenv("TPT_HIP_CAUSAL_ATTN");
@@ -682,13 +682,13 @@ int tpt_model::batched_layers(int T, int p0, int l0, int l1) {
     a.mode = GEMM_Q8K; a.af = pf_af; a.ad = pf_ad; a.as16 = pf_as16;
     return launch_act_prep(a, stream);
   };
-  auto gemm = [&](const uint8_t* w, int K, int N, float* y, int ldy, const float* resid) {
+  auto gemm = [&](int type, const uint8_t* w, int K, int N, float* y, int ldy, const float* resid) {
     GemmArgs g;
-    g.M = T; g.N = N; g.K = K; g.mode = GEMM_Q8K;
-    g.w = w; g.w_stride = row_bytes(TPT_TYPE_Q4_K, K);
+    g.M = T; g.N = N; g.K = K; g.mode = GEMM_Q8K; g.wtype = type;
+    g.w = w; g.w_stride = row_bytes(type, K);
     g.af = pf_af; g.ad = pf_ad; g.as16 = pf_as16;
     g.y = y; g.ldy = ldy; g.resid = resid; g.ldr = ldy;
-    return launch_gemm_q4k(g, stream);
+    return launch_gemm(g, stream);
   };
   for (int l = l0; l < l1; l++) {
     const Layer& L = layers[l];
@@ -697,10 +697,10 @@ int tpt_model::batched_layers(int T, int p0, int l0, int l1) {
     if ((rc = prep(pf_x, nullptr, H, L.attn_norm))) return rc;
     const int ldq = qd + 2 * kd;
     if (L.qkv_adjacent) {
-      if ((rc = gemm(L.q, H, ldq, pf_qkv, ldq, nullptr))) return rc;
+      if ((rc = gemm(L.tq, L.q, H, ldq, pf_qkv, ldq, nullptr))) return rc;
     } else {
-      if ((rc = gemm(L.q, H, qd, pf_qkv, ldq, nullptr)) || (rc = gemm(L.k, H, kd, pf_qkv + qd, ldq, nullptr)) ||
-          (rc = gemm(L.v, H, kd, pf_qkv + qd + kd, ldq, nullptr)))
+      if ((rc = gemm(L.tq, L.q, H, qd, pf_qkv, ldq, nullptr)) || (rc = gemm(L.tk, L.k, H, kd, pf_qkv + qd, ldq, nullptr)) ||
+          (rc = gemm(L.tv, L.v, H, kd, pf_qkv + qd + kd, ldq, nullptr)))
         return rc;
     }
     QkvPostArgs qp;
@@ -715,11 +715,11 @@ int tpt_model::batched_layers(int T, int p0, int l0, int l1) {
     rc = causal_mfma && attn_causal_mfma_supported(at) ? launch_attn_causal_mfma(at, stream)
                                                        : launch_attn_decode(at, stream);
     if (rc) return rc;
-    if ((rc = prep(pf_att, nullptr, qd, nullptr)) || (rc = gemm(L.o, qd, H, pf_x, H, pf_x))) return rc;
-    if ((rc = prep(pf_x, nullptr, H, L.ffn_norm)) || (rc = gemm(L.gate, H, F, pf_g, F, nullptr)) ||
-        (rc = gemm(L.up, H, F, pf_u, F, nullptr)))
+    if ((rc = prep(pf_att, nullptr, qd, nullptr)) || (rc = gemm(L.to, L.o, qd, H, pf_x, H, pf_x))) return rc;
+    if ((rc = prep(pf_x, nullptr, H, L.ffn_norm)) || (rc = gemm(L.tg, L.gate, H, F, pf_g, F, nullptr)) ||
+        (rc = gemm(L.tu, L.up, H, F, pf_u, F, nullptr)))
       return rc;
-    if ((rc = prep(pf_g, pf_u, F, nullptr)) || (rc = gemm(L.down, F, H, pf_x, H, pf_x))) return rc;
+    if ((rc = prep(pf_g, pf_u, F, nullptr)) || (rc = gemm(L.td, L.down, F, H, pf_x, H, pf_x))) return rc;
   }
   return TPT_OK;
 }

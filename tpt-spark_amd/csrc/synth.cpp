@@ -234,6 +234,9 @@ typedef struct {
   float rope_base, rms_eps, init_std;
   int type_matrix, type_embd, type_out;
   uint32_t eos_token_id;
+  // nonzero: attn_v and ffn_down of the layers llama.cpp's Q4_K_M recipe gives more bits
+  // (the first and last eighth of the layers and every third layer between) get this type
+  int type_more_bits;
 } tpt_synth_cfg;
 
 // Quantize n floats (a whole number of blocks) into GGUF blocks of `type`.
@@ -260,17 +263,20 @@ int tpt_synth_write_llama(const char* path, const tpt_synth_cfg* c, uint64_t see
   add("token_embd.weight", c->type_embd, H, V, 0);
   add("output_norm.weight", T_F32, H, 1, 1);
   add("output.weight", c->type_out, H, V, 0);
-  for (int l = 0; l < c->n_layers; l++) {
+  const int nl = c->n_layers;
+  for (int l = 0; l < nl; l++) {
     const std::string p = "blk." + std::to_string(l) + ".";
+    const bool more = c->type_more_bits && (l < nl / 8 || l >= 7 * nl / 8 || (l - nl / 8) % 3 == 2);
+    const int tvd = more ? c->type_more_bits : c->type_matrix;
     add(p + "attn_norm.weight", T_F32, H, 1, 1);
     add(p + "attn_q.weight", c->type_matrix, H, qd, 0);
     add(p + "attn_k.weight", c->type_matrix, H, kd, 0);
-    add(p + "attn_v.weight", c->type_matrix, H, kd, 0);
+    add(p + "attn_v.weight", tvd, H, kd, 0);
     add(p + "attn_output.weight", c->type_matrix, qd, H, 0);
     add(p + "ffn_norm.weight", T_F32, H, 1, 1);
     add(p + "ffn_gate.weight", c->type_matrix, H, F, 0);
     add(p + "ffn_up.weight", c->type_matrix, H, F, 0);
-    add(p + "ffn_down.weight", c->type_matrix, F, H, 0);
+    add(p + "ffn_down.weight", tvd, F, H, 0);
   }
   const uint64_t ALIGN = 32;
   uint64_t off = 0;

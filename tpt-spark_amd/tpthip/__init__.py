@@ -103,6 +103,7 @@ EXPORTS = {
     "tpt_common_prefix_len": ([P, SZ, P, SZ], SZ),
     "tpt_bench_gemv": ([P, I32, P, I32, P, P, I32, I32, I32, P], I32),
     "tpt_attn_prefill": ([P, P, P, P, I32, P, I32, I32, I32, I32, I32, I32, I32], I32),
+    "tpt_bench_attn_prefill": ([P, P, P, P, I32, P, I32, I32, I32, I32, I32, I32, I32, P], I32),
     "tpt_bench_attn": ([P, P, P, P, I32, I32, P, I32, I32, I32, I32, I32, I32, I32, P], I32),
     "tpt_bench_copy": ([P, P, P, SZ, I32, P], I32),
     "tpt_gemm": ([P, I32, P, P, P, I32, I32, I32, I32], I32),
@@ -287,6 +288,14 @@ class Context:
         ms = C.c_float()
         check(lib().tpt_bench_attn(self.h, qbuf.ptr, ks, vs, len(kbufs), kv_type, obuf.ptr, nq, nkv,
                                    hd, L, L_stride, n_chunks, iters, C.byref(ms)))
+        return ms.value
+
+    def bench_attn_prefill(self, qbuf, kbuf, vbuf, obuf, nq, nkv, hd, L0, T, L_stride, iters,
+                           kv_type=TYPE_F16):
+        """Event-timed back-to-back launches of the matrix-core causal attention; returns ms."""
+        ms = C.c_float()
+        check(lib().tpt_bench_attn_prefill(self.h, qbuf.ptr, kbuf.ptr, vbuf.ptr, kv_type, obuf.ptr,
+                                           nq, nkv, hd, L0, T, L_stride, iters, C.byref(ms)))
         return ms.value
 
     def bench_gemv(self, qtype, wbufs, xbuf, ybuf, K, N, iters):

@@ -17,7 +17,7 @@ class SynthCfg(C.Structure):
                                        "context_length")] + \
                [("rope_base", C.c_float), ("rms_eps", C.c_float), ("init_std", C.c_float)] + \
                [(n, C.c_int) for n in ("type_matrix", "type_embd", "type_out")] + \
-               [("eos_token_id", C.c_uint32)]
+               [("eos_token_id", C.c_uint32), ("type_more_bits", C.c_int)]
 
 
 def lib():
@@ -44,10 +44,12 @@ TINY = dict(n_layers=2, embed=256, n_heads=4, n_kv_heads=2, ffn=512, vocab=1024,
 
 
 def write_llama(path, cfg, seed=0, nthreads=0, init_std=0.02, type_matrix=TYPE_Q4_K,
-                type_embd=TYPE_Q6_K, type_out=TYPE_Q6_K):
+                type_embd=TYPE_Q6_K, type_out=TYPE_Q6_K, type_more_bits=0):
+    """type_more_bits (e.g. TYPE_Q6_K): attn_v and ffn_down of the layers llama.cpp's Q4_K_M
+    recipe gives more bits get that type, as in a real Q4_K_M file."""
     c = SynthCfg(cfg["n_layers"], cfg["embed"], cfg["n_heads"], cfg["n_kv_heads"], cfg["ffn"],
                  cfg["vocab"], cfg["context_length"], cfg["rope_base"], cfg["rms_eps"], init_std,
-                 type_matrix, type_embd, type_out, cfg.get("eos_token_id", 0))
+                 type_matrix, type_embd, type_out, cfg.get("eos_token_id", 0), type_more_bits)
     rc = lib().tpt_synth_write_llama(path.encode(), C.byref(c), seed, nthreads)
     if rc:
         raise RuntimeError(f"tpt_synth_write_llama({path}) failed: {rc}")
