@@ -20,8 +20,9 @@
 //    exact); isum = 64 hi + lo rounds once.
 //  * GEMM_F16: the tile is dequantized into LDS as fp16 (Q4_K: d*sc*q - dmin*m, Q6_K:
 //    d*sc*(q - 32), rounded to fp16), the activation is fp16, one fp32 MFMA chain over all of K.
-// Tiling (MI355X: 160 KB LDS, wave64, v_mfma_f32_32x32x16_f16): 256 threads, a 128 x 128 tile
-// of Y per workgroup, each wave 64 x 64 (2 x 2 MFMA tiles).  K advances half a super-block (128)
+// Tiling (MI355X: 160 KB LDS, wave64, v_mfma_f32_32x32x16_f16): 512 threads, a 128 x 128 tile
+// of Y per workgroup, each wave 64 x 32 (2 x 1 MFMA tiles), two waves per SIMD so that one
+// wave's weight decode and block scaling run while the other's MFMAs do.  K advances half a super-block (128)
 // per step through a double-buffered LDS tile: while a step's MFMAs read one buffer, the next
 // step's weights are decoded into the other and the step after that is in flight from HBM, so
 // the Q4_K decode overlaps the matrix cores instead of alternating with them.  The activation
@@ -40,7 +41,7 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int GT = 256;          // threads per workgroup
+constexpr int GT = 512;          // threads per workgroup
 constexpr int BM = 128, BN = 128, BK = 128;
 constexpr int LDK = BK + 2;      // fp16 per LDS row: a 4-byte pad spreads the MFMA operand reads over
                                  // the banks (measured: 16 B of pad left 9x the bank-conflict cycles)
@@ -61,23 +62,25 @@ struct GemmSmem {
   GemmBlock blk[2];              // by super-block parity
 };
 
-// Registers one thread stages for a K step (thread = row r, half hf of the step's 128 elements):
-// 64 fp16 activation values and the weight bytes of those 64 elements; in the first half of a
-// super-block also the row's block scale (and, for Q4_K, 8 of its per-16 sums).
-//  * Q4_K: the block header (d, dmin, packed scales) and the group's 32 qs bytes.
-//  * Q6_K: the half's 64 ql bytes, 32 qh bytes, 8 int8 scales and d (210-byte blocks are only
-//    2-byte aligned: 16-bit loads).
+// Registers one thread stages for a K step (thread = row r = tid / 4, quarter qt = tid % 4 of
+// the step's 128 elements): 32 fp16 activation values and the weight bytes of those 32
+// elements; in the first half of a super-block also the row's block scale (and, for Q4_K, 4 of
+// its per-16 sums).
+//  * Q4_K: the block header (d, dmin, packed scales) and 16 qs bytes of group 2 hb + qt / 2
+//    (the low nibbles are 16 elements of sub-block 2g, the high nibbles 16 of sub-block 2g + 1).
+//  * Q6_K: quad qt of the half: its 32 ql bytes, the half's 32 qh bytes, the half's 8 int8
+//    scales and d (210-byte blocks are only 2-byte aligned: 16-bit loads).
 template <int WT> struct Stage;
 template <> struct Stage<TPT_TYPE_Q4_K> {
-  u32x4 a[8];
+  u32x4 a[4];
   u32x4 h;
-  u32x4 q[2];
-  u32x4 a16;
+  u32x4 q;
+  u32x2 a16;
   float dx;
 };
 template <> struct Stage<TPT_TYPE_Q6_K> {
-  u32x4 a[8];
-  u32x4 ql[4];
+  u32x4 a[4];
+  u32x4 ql[2];
   u32x4 qh[2];
   u32x2 sc;
   uint32_t d;
@@ -100,22 +103,20 @@ __device__ __forceinline__ void get_scale_min(const u32x4& h, int j, int* sc, in
 // step = 2 kb + hb: super-block kb, half hb
 template <int WT, int MODE, int HB>
 __device__ __forceinline__ void stage_load(const GemmArgs& g, int m0, int n0, int kb, Stage<WT>& st) {
-  const int tid = threadIdx.x, r = tid >> 1, hf = tid & 1;
+  const int tid = threadIdx.x, r = tid >> 2, qt = tid & 3;
   int m = m0 + r;
   if (m >= g.M) m = g.M - 1;
   int n = n0 + r;
   if (n >= g.N) n = g.N - 1;
-  const u32x4* src = (const u32x4*)(g.af + (size_t)m * g.K + (size_t)kb * 256 + 128 * HB + 64 * hf);
+  const u32x4* src = (const u32x4*)(g.af + (size_t)m * g.K + (size_t)kb * 256 + 128 * HB + 32 * qt);
 #pragma unroll
-  for (int i = 0; i < 8; i++) st.a[i] = src[i];
+  for (int i = 0; i < 4; i++) st.a[i] = src[i];
   if constexpr (WT == TPT_TYPE_Q4_K) {
     const uint8_t* blk = g.w + (size_t)n * g.w_stride + (size_t)kb * 144;
     st.h = *(const u32x4*)blk;
-    const u32x4* qs = (const u32x4*)(blk + 16 + 32 * (2 * HB + hf));
-    st.q[0] = qs[0];
-    st.q[1] = qs[1];
+    st.q = *(const u32x4*)(blk + 16 + 32 * (2 * HB + (qt >> 1)) + 16 * (qt & 1));
     if constexpr (MODE == GEMM_Q8K && HB == 0)
-      st.a16 = *(const u32x4*)(g.as16 + (size_t)m * (g.K / 16) + kb * 16 + 8 * hf);
+      st.a16 = *(const u32x2*)(g.as16 + (size_t)m * (g.K / 16) + kb * 16 + 4 * qt);
   } else {
     // 2-byte aligned rows: 32-bit words assembled from aligned 16-bit loads
     const uint16_t* blk = (const uint16_t*)(g.w + (size_t)n * g.w_stride + (size_t)kb * 210);
@@ -125,8 +126,9 @@ __device__ __forceinline__ void stage_load(const GemmArgs& g, int m0, int n0, in
     auto w128 = [&](int byte_off) {
       return u32x4{w32(byte_off), w32(byte_off + 4), w32(byte_off + 8), w32(byte_off + 12)};
     };
+    const int qlo = 64 * HB + 32 * (qt & 1);  // ql bytes of quad qt
 #pragma unroll
-    for (int i = 0; i < 4; i++) st.ql[i] = w128(64 * HB + 16 * i);
+    for (int i = 0; i < 2; i++) st.ql[i] = w128(qlo + 16 * i);
 #pragma unroll
     for (int i = 0; i < 2; i++) st.qh[i] = w128(128 + 32 * HB + 16 * i);
     st.sc = u32x2{w32(192 + 8 * HB), w32(196 + 8 * HB)};
@@ -140,22 +142,21 @@ typedef short short2 __attribute__((ext_vector_type(2)));
 
 template <int WT, int MODE, int HB>
 __device__ __forceinline__ void stage_store(const Stage<WT>& st, GemmTile& T, GemmBlock& B) {
-  const int tid = threadIdx.x, r = tid >> 1, hf = tid & 1;
+  const int tid = threadIdx.x, r = tid >> 2, qt = tid & 3;
 #pragma unroll
-  for (int i = 0; i < 8; i++) *(u32x4*)&T.a[r][64 * hf + 8 * i] = st.a[i];
-  const int e0 = 64 * hf;
+  for (int i = 0; i < 4; i++) *(u32x4*)&T.a[r][32 * qt + 8 * i] = st.a[i];
   float d, dmin = 0.f;
   if constexpr (WT == TPT_TYPE_Q4_K) {
-    // weight row r, group g = 2 HB + hf: qs[32g + l] holds element 64g + l (low nibble,
-    // sub-block 2g) and 64g + 32 + l (high nibble, sub-block 2g + 1); in the step tile at
-    // 64 hf + l, + 32
-    const int g = 2 * HB + hf;
+    // weight row r, group g = 2 HB + qt / 2: qs[32g + l] holds element 64g + l (low nibble,
+    // sub-block 2g) and 64g + 32 + l (high nibble, sub-block 2g + 1); this thread has
+    // l = 16 (qt % 2) .. + 15, tile columns c0 + l' and c0 + 32 + l'
+    const int g = 2 * HB + (qt >> 1);
+    const int c0 = 64 * (qt >> 1) + 16 * (qt & 1);
     d = h2f((uint16_t)(st.h.x & 0xffff));
     dmin = h2f((uint16_t)(st.h.x >> 16));
     int sc0, m0, sc1, m1;
     get_scale_min(st.h, 2 * g, &sc0, &m0);
     get_scale_min(st.h, 2 * g + 1, &sc1, &m1);
-    const uint32_t w[8] = {st.q[0].x, st.q[0].y, st.q[0].z, st.q[0].w, st.q[1].x, st.q[1].y, st.q[1].z, st.q[1].w};
     if constexpr (MODE == GEMM_Q8K) {
       // the integers sc * q two at a time in packed fp16, all exact: a byte pair (b, b') moved
       // to the two halves, its nibbles ORed into the mantissa of 1024.0 (0x6400) give 1024 + q,
@@ -167,11 +168,11 @@ __device__ __forceinline__ void stage_store(const Stage<WT>& st, GemmTile& T, Ge
         return __builtin_bit_cast(uint32_t, v * sc);
       };
 #pragma unroll
-      for (int c = 0; c < 4; c++) {  // 8 consecutive elements per 16-byte store
+      for (int c = 0; c < 2; c++) {  // 8 consecutive elements per 16-byte store
         u32x4 lo, hi;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-          const uint32_t x = w[2 * c + h];
+          const uint32_t x = st.q[2 * c + h];
           const uint32_t p01 = __builtin_amdgcn_perm(0u, x, 0x0c010c00u);  // bytes 0, 1 -> halves
           const uint32_t p23 = __builtin_amdgcn_perm(0u, x, 0x0c030c02u);  // bytes 2, 3 -> halves
           lo[2 * h] = dec(p01, s0);
@@ -179,92 +180,83 @@ __device__ __forceinline__ void stage_store(const Stage<WT>& st, GemmTile& T, Ge
           hi[2 * h] = dec(p01 >> 4, s1);
           hi[2 * h + 1] = dec(p23 >> 4, s1);
         }
-        *(u32x4*)&T.b[r][e0 + 8 * c] = lo;
-        *(u32x4*)&T.b[r][e0 + 32 + 8 * c] = hi;
+        *(u32x4*)&T.b[r][c0 + 8 * c] = lo;
+        *(u32x4*)&T.b[r][c0 + 32 + 8 * c] = hi;
       }
       // mins of sub-blocks 2g, 2g + 1, each for its two 16-element halves (16-sums 8g .. 8g+3)
-      B.b16[r][4 * g] = (_Float16)m0;
-      B.b16[r][4 * g + 1] = (_Float16)m0;
-      B.b16[r][4 * g + 2] = (_Float16)m1;
-      B.b16[r][4 * g + 3] = (_Float16)m1;
+      const half2 mm0 = {(_Float16)m0, (_Float16)m0}, mm1 = {(_Float16)m1, (_Float16)m1};
+      *(u32x2*)&B.b16[r][4 * g] = u32x2{__builtin_bit_cast(uint32_t, mm0), __builtin_bit_cast(uint32_t, mm1)};
       if constexpr (HB == 0) {
-        const uint32_t b[4] = {st.a16.x, st.a16.y, st.a16.z, st.a16.w};
-        half8 v;
+        u32x2 v;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-          v[2 * j] = (_Float16)(int16_t)(b[j] & 0xffff);
-          v[2 * j + 1] = (_Float16)(int16_t)(b[j] >> 16);
+        for (int j = 0; j < 2; j++) {
+          const half2 p = {(_Float16)(int16_t)(st.a16[j] & 0xffff), (_Float16)(int16_t)(st.a16[j] >> 16)};
+          v[j] = __builtin_bit_cast(uint32_t, p);
         }
-        *(half8*)&B.a16[r][8 * hf] = v;
+        *(u32x2*)&B.a16[r][4 * qt] = v;
       }
     } else {
+      const float d1 = d * (float)sc0, mm1 = dmin * (float)m0;
+      const float d2 = d * (float)sc1, mm2 = dmin * (float)m1;
 #pragma unroll
-      for (int c = 0; c < 4; c++) {  // 8 consecutive elements per half8 store
+      for (int c = 0; c < 2; c++) {  // 8 consecutive elements per half8 store
         half8 lo, hi;
 #pragma unroll
         for (int t = 0; t < 8; t++) {
-          const uint32_t byte = (w[2 * c + t / 4] >> (8 * (t % 4))) & 0xff;
-          const int ql = byte & 0xF, qh = byte >> 4;
-          const float d1 = d * (float)sc0, mm1 = dmin * (float)m0;
-          const float d2 = d * (float)sc1, mm2 = dmin * (float)m1;
-          lo[t] = (_Float16)(d1 * (float)ql - mm1);
-          hi[t] = (_Float16)(d2 * (float)qh - mm2);
+          const uint32_t byte = (st.q[2 * c + t / 4] >> (8 * (t % 4))) & 0xff;
+          lo[t] = (_Float16)(d1 * (float)(byte & 0xF) - mm1);
+          hi[t] = (_Float16)(d2 * (float)(byte >> 4) - mm2);
         }
-        *(half8*)&T.b[r][e0 + 8 * c] = lo;
-        *(half8*)&T.b[r][e0 + 32 + 8 * c] = hi;
+        *(half8*)&T.b[r][c0 + 8 * c] = lo;
+        *(half8*)&T.b[r][c0 + 32 + 8 * c] = hi;
       }
     }
   } else {
     // Q6_K half HB of a super-block, elements 32 Q + l of the half (quad Q, l < 32):
     //   q = ((ql[32 (Q & 1) + l] >> 4 (Q >= 2)) & 15) | ((qh[l] >> 2 Q) & 3) << 4,
     //   scale sc[2 Q + l / 16], weight d * scale * (q - 32).
-    // Thread hf holds quads 2 hf (tile columns 64 hf + l) and 2 hf + 1 (64 hf + 32 + l).
+    // Thread qt holds quad Q = qt (tile columns 32 qt + l).
     d = h2f((uint16_t)st.d);
-    const uint32_t scw = hf ? st.sc[1] : st.sc[0];  // scales 4 hf .. 4 hf + 3
-    int sc[4];
+    const int sh = 4 * (qt >> 1), shh = 2 * qt;
+    const uint32_t scw = qt >= 2 ? st.sc[1] : st.sc[0];  // scales 4 (qt / 2) .. + 3
+    const int sA = (int)(int8_t)(scw >> (16 * (qt & 1))), sB = (int)(int8_t)(scw >> (16 * (qt & 1) + 8));
 #pragma unroll
-    for (int i = 0; i < 4; i++) sc[i] = (int)(int8_t)(scw >> (8 * i));
-    const int sh = 4 * hf;
+    for (int c = 0; c < 4; c++) {   // elements 8c .. 8c + 7 of the quad
+      const int s = c < 2 ? sA : sB;
+      uint32_t qv[2];
 #pragma unroll
-    for (int qq = 0; qq < 2; qq++) {  // quad 2 hf + qq
-#pragma unroll
-      for (int c = 0; c < 4; c++) {   // elements 8c .. 8c + 7 of the quad
-        const int s = sc[2 * qq + c / 2];
-        uint32_t qv[2];
+      for (int h = 0; h < 2; h++) {
+        const int wi = 2 * c + h;  // ql / qh word of elements 4 wi .. 4 wi + 3
+        const uint32_t x = st.ql[wi / 4][wi % 4], hb = st.qh[wi / 4][wi % 4];
+        qv[h] = ((x >> sh) & 0x0F0F0F0Fu) | (((hb >> shh) & 0x03030303u) << 4);
+      }
+      if constexpr (MODE == GEMM_Q8K) {
+        // w = s * (q - 32) in [-4064, 4096] as w + 4096 = 64 u + w0 (u <= 128, w0 < 64), stored
+        // per element as the bytes (w0, u): the MFMA operands w1 = u - 64 and w0 are then exact
+        // fp16 values with w = 64 w1 + w0
+        const short2 s2 = {(short)s, (short)s}, c2 = {(short)(4096 - 32 * s), (short)(4096 - 32 * s)};
+        u32x4 o;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-          const int wi = 8 * qq + 2 * c + h;  // ql word of the half; qh word 2c + h
-          const uint32_t x = st.ql[wi / 4][wi % 4], hb = st.qh[(2 * c + h) / 4][(2 * c + h) % 4];
-          qv[h] = ((x >> sh) & 0x0F0F0F0Fu) | (((hb >> (sh + 2 * qq)) & 0x03030303u) << 4);
+          const uint32_t p01 = __builtin_amdgcn_perm(0u, qv[h], 0x0c010c00u);
+          const uint32_t p23 = __builtin_amdgcn_perm(0u, qv[h], 0x0c030c02u);
+          const uint32_t w01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(short2, p01) * s2 + c2);
+          const uint32_t w23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(short2, p23) * s2 + c2);
+          o[2 * h] = ((w01 << 2) & 0xFF00FF00u) | (w01 & 0x003F003Fu);
+          o[2 * h + 1] = ((w23 << 2) & 0xFF00FF00u) | (w23 & 0x003F003Fu);
         }
-        if constexpr (MODE == GEMM_Q8K) {
-          // w = s * (q - 32) in [-4064, 4096] as w + 4096 = 64 u + w0 (u <= 128, w0 < 64), stored
-          // per element as the bytes (w0, u): the MFMA operands w1 = u - 64 and w0 are then
-          // exact fp16 values with w = 64 w1 + w0
-          const short2 s2 = {(short)s, (short)s}, c2 = {(short)(4096 - 32 * s), (short)(4096 - 32 * s)};
-          u32x4 o;
+        *(u32x4*)&T.b[r][32 * qt + 8 * c] = o;
+      } else {
+        const float ds = d * (float)s;
+        half8 v;
 #pragma unroll
-          for (int h = 0; h < 2; h++) {
-            const uint32_t p01 = __builtin_amdgcn_perm(0u, qv[h], 0x0c010c00u);
-            const uint32_t p23 = __builtin_amdgcn_perm(0u, qv[h], 0x0c030c02u);
-            const uint32_t w01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(short2, p01) * s2 + c2);
-            const uint32_t w23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(short2, p23) * s2 + c2);
-            o[2 * h] = ((w01 << 2) & 0xFF00FF00u) | (w01 & 0x003F003Fu);
-            o[2 * h + 1] = ((w23 << 2) & 0xFF00FF00u) | (w23 & 0x003F003Fu);
-          }
-          *(u32x4*)&T.b[r][e0 + 32 * qq + 8 * c] = o;
-        } else {
-          const float ds = d * (float)s;
-          half8 v;
-#pragma unroll
-          for (int t = 0; t < 8; t++) v[t] = (_Float16)(ds * (float)((int)((qv[t / 4] >> (8 * (t % 4))) & 0xff) - 32));
-          *(half8*)&T.b[r][e0 + 32 * qq + 8 * c] = v;
-        }
+        for (int t = 0; t < 8; t++) v[t] = (_Float16)(ds * (float)((int)((qv[t / 4] >> (8 * (t % 4))) & 0xff) - 32));
+        *(half8*)&T.b[r][32 * qt + 8 * c] = v;
       }
     }
   }
   if constexpr (MODE == GEMM_Q8K && HB == 0) {
-    // both threads of the row hold the same values: the duplicate stores keep the step one
+    // the four threads of the row hold the same values: the duplicate stores keep the step one
     // basic block for the scheduler
     B.dx[r] = st.dx;
     B.dw[r] = d;
@@ -272,29 +264,13 @@ __device__ __forceinline__ void stage_store(const Stage<WT>& st, GemmTile& T, Ge
   }
 }
 
-// Instruction interleave of one K step (one basic block: the staging of the next step and this
-// step's MFMAs): per 16-element slice of K, its operand reads and MFMAs, then a share of the
-// staging work (the weight decode's VALU, its LDS writes, the global loads of the step after), so
-// the decode runs while the matrix cores work instead of after them.
-template <int NMFMA>
-__device__ __forceinline__ void interleave_step() {
-#pragma unroll
-  for (int i = 0; i < BK / 16; i++) {
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);      // LDS reads (operands)
-    __builtin_amdgcn_sched_group_barrier(0x008, NMFMA, 0);  // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x002, 48, 0);     // VALU
-    __builtin_amdgcn_sched_group_barrier(0x200, 3, 0);      // LDS writes
-    __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);      // global loads
-  }
-}
-
-// One K step of MFMAs on tile T (each wave: 64 x 64 as 2 x 2 tiles of 32 x 32).  Q4_K and the
+// One K step of MFMAs on tile T (each wave: 64 x 32 as 2 x 1 tiles of 32 x 32).  Q4_K and the
 // fp16 mode: acc += A . B.  Q6_K in GEMM_Q8K mode: the B tile holds the bytes (w0, u) of each
 // weight; two exact chains, hi += A . (u - 64) and lo += A . w0.
 template <int WT, int MODE>
-__device__ __forceinline__ void mfma_step(const GemmTile& T, floatx16 (&acc)[2][2], floatx16 (&lo)[2][2]) {
+__device__ __forceinline__ void mfma_step(const GemmTile& T, floatx16 (&acc)[2], floatx16 (&lo)[2]) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int wm = wid >> 1, wn = wid & 1;
+  const int wm = wid >> 2, wn = wid & 3;
   const int lr = lane & 31, lk = 8 * (lane >> 5);
 #pragma unroll
   for (int kk = 0; kk < BK; kk += 16) {
@@ -302,35 +278,24 @@ __device__ __forceinline__ void mfma_step(const GemmTile& T, floatx16 (&acc)[2][
 #pragma unroll
     for (int i = 0; i < 2; i++) a[i] = *(const half8*)&T.a[64 * wm + 32 * i + lr][kk + lk];
     if constexpr (WT == TPT_TYPE_Q6_K && MODE == GEMM_Q8K) {
-      half8 bh[2], bl[2];
+      const u32x4 raw = *(const u32x4*)&T.b[32 * wn + lr][kk + lk];
+      const half2 k1088 = {(_Float16)1088.f, (_Float16)1088.f}, k1024 = {(_Float16)1024.f, (_Float16)1024.f};
+      u32x4 h, l;
 #pragma unroll
-      for (int j = 0; j < 2; j++) {
-        const u32x4 raw = *(const u32x4*)&T.b[64 * wn + 32 * j + lr][kk + lk];
-        const half2 k1088 = {(_Float16)1088.f, (_Float16)1088.f}, k1024 = {(_Float16)1024.f, (_Float16)1024.f};
-        u32x4 h, l;
-#pragma unroll
-        for (int c = 0; c < 4; c++) {  // bytes (w0, u) of two weights -> fp16 1024 + u, 1024 + w0
-          h[c] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, __builtin_amdgcn_perm(0x64646464u, raw[c], 0x04030401u)) - k1088);
-          l[c] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, __builtin_amdgcn_perm(0x64646464u, raw[c], 0x04020400u)) - k1024);
-        }
-        bh[j] = __builtin_bit_cast(half8, h);
-        bl[j] = __builtin_bit_cast(half8, l);
+      for (int c = 0; c < 4; c++) {  // bytes (w0, u) of two weights -> fp16 1024 + u, 1024 + w0
+        h[c] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, __builtin_amdgcn_perm(0x64646464u, raw[c], 0x04030401u)) - k1088);
+        l[c] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, __builtin_amdgcn_perm(0x64646464u, raw[c], 0x04020400u)) - k1024);
       }
+      const half8 bh = __builtin_bit_cast(half8, h), bl = __builtin_bit_cast(half8, l);
 #pragma unroll
-      for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bh[j], acc[i][j], 0, 0, 0);
-          lo[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bl[j], lo[i][j], 0, 0, 0);
-        }
+      for (int i = 0; i < 2; i++) {
+        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bh, acc[i], 0, 0, 0);
+        lo[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bl, lo[i], 0, 0, 0);
+      }
     } else {
-      half8 b[2];
+      const half8 b = *(const half8*)&T.b[32 * wn + lr][kk + lk];
 #pragma unroll
-      for (int j = 0; j < 2; j++) b[j] = *(const half8*)&T.b[64 * wn + 32 * j + lr][kk + lk];
-#pragma unroll
-      for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+      for (int i = 0; i < 2; i++) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b, acc[i], 0, 0, 0);
     }
   }
 }
@@ -340,78 +305,70 @@ __device__ __forceinline__ void mfma_step(const GemmTile& T, floatx16 (&acc)[2][
 // sum_j m_j * bsum_j on the matrix cores (K = 16, exact) enters as - (dmin_w d_x) msum.  Q6_K:
 // isum = 64 hi + lo (64 hi exact, one rounding); no mins term.
 template <int WT>
-__device__ __forceinline__ void block_end(const GemmBlock& B, floatx16 (&acc0)[2][2], floatx16 (&acc1)[2][2],
-                                          floatx16 (&out)[2][2]) {
+__device__ __forceinline__ void block_end(const GemmBlock& B, floatx16 (&acc0)[2], floatx16 (&acc1)[2],
+                                          floatx16 (&out)[2]) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int wm = wid >> 1, wn = wid & 1;
+  const int wm = wid >> 2, wn = wid & 3;
   const int lr = lane & 31, lk = 8 * (lane >> 5);
-  half8 a[2], b[2];
+  const int col = 32 * wn + lr;
+  const float dw = B.dw[col];
+  half8 b;
+  float dm = 0.f;
   if constexpr (WT == TPT_TYPE_Q4_K) {
-#pragma unroll
-    for (int i = 0; i < 2; i++) a[i] = *(const half8*)&B.a16[64 * wm + 32 * i + lr][lk];
-#pragma unroll
-    for (int j = 0; j < 2; j++) b[j] = *(const half8*)&B.b16[64 * wn + 32 * j + lr][lk];
+    b = *(const half8*)&B.b16[col][lk];
+    dm = B.dm[col];
   }
-  // the lane's 16 rows of tile i are 4 runs of 4 consecutive rows: one float4 each
-  float dxs[2][16];
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < 2; i++) {
+    // the lane's 16 rows of tile i are 4 runs of 4 consecutive rows: one float4 each
+    float dxs[16];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
       const float4 v = *(const float4*)&B.dx[64 * wm + 32 * i + q * 8 + (lane >> 5) * 4];
-      dxs[i][4 * q] = v.x; dxs[i][4 * q + 1] = v.y; dxs[i][4 * q + 2] = v.z; dxs[i][4 * q + 3] = v.w;
+      dxs[4 * q] = v.x; dxs[4 * q + 1] = v.y; dxs[4 * q + 2] = v.z; dxs[4 * q + 3] = v.w;
     }
+    if constexpr (WT == TPT_TYPE_Q4_K) {
+      const half8 a = *(const half8*)&B.a16[64 * wm + 32 * i + lr][lk];
+      const floatx16 accm = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, floatx16{}, 0, 0, 0);
 #pragma unroll
-  for (int i = 0; i < 2; i++)
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int col = 64 * wn + 32 * j + lr;
-      const float dw = B.dw[col];
-      if constexpr (WT == TPT_TYPE_Q4_K) {
-        const floatx16 accm = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], floatx16{}, 0, 0, 0);
-        const float dm = B.dm[col];
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-          const float dx = dxs[i][e];
-          const float isum = acc0[i][j][e] + acc1[i][j][e];
-          const float dd = dw * dx, ddm = dm * dx;
-          const float v = dd * isum - ddm * accm[e];
-          out[i][j][e] = out[i][j][e] + v;
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-          const float isum = fmaf(64.f, acc0[i][j][e], acc1[i][j][e]);
-          out[i][j][e] = out[i][j][e] + (dw * dxs[i][e]) * isum;
-        }
+      for (int e = 0; e < 16; e++) {
+        const float dx = dxs[e];
+        const float isum = acc0[i][e] + acc1[i][e];
+        const float dd = dw * dx, ddm = dm * dx;
+        const float v = dd * isum - ddm * accm[e];
+        out[i][e] = out[i][e] + v;
       }
-      acc0[i][j] = floatx16{};
-      acc1[i][j] = floatx16{};
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const float isum = fmaf(64.f, acc0[i][e], acc1[i][e]);
+        out[i][e] = out[i][e] + (dw * dxs[e]) * isum;
+      }
     }
+    acc0[i] = floatx16{};
+    acc1[i] = floatx16{};
+  }
 }
 
 template <int WT, int MODE>
 __global__ void __launch_bounds__(GT, 1) gemm_kernel(const GemmArgs g) {
   __shared__ GemmSmem s;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int wm = wid >> 1, wn = wid & 1;  // wave tile: rows 64 wm .., cols 64 wn ..
+  const int wm = wid >> 2, wn = wid & 3;  // wave tile: rows 64 wm .., cols 32 wn ..
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   const int nkb = g.K / 256;
   const int lr = lane & 31;
   // chains: Q4_K q8k acc0 / acc1 = the two halves of a super-block; Q6_K q8k acc0 / acc1 =
   // hi / lo over the whole super-block; fp16 mode: out directly
   constexpr bool Q6 = WT == TPT_TYPE_Q6_K;
-  constexpr int NMFMA = Q6 && MODE == GEMM_Q8K ? 8 : 4;
 
-  floatx16 out[2][2], acc0[2][2], acc1[2][2];
+  floatx16 out[2], acc0[2], acc1[2];
 #pragma unroll
-  for (int i = 0; i < 2; i++)
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-      out[i][j] = floatx16{};
-      acc0[i][j] = floatx16{};
-      acc1[i][j] = floatx16{};
-    }
+  for (int i = 0; i < 2; i++) {
+    out[i] = floatx16{};
+    acc0[i] = floatx16{};
+    acc1[i] = floatx16{};
+  }
 
   // prologue: step 0 in LDS, step 1 in registers
   Stage<WT> st;
@@ -429,7 +386,6 @@ __global__ void __launch_bounds__(GT, 1) gemm_kernel(const GemmArgs g) {
     stage_load<WT, MODE, 0>(g, m0, n0, kn, st);
     if constexpr (MODE == GEMM_Q8K) mfma_step<WT, MODE>(s.t[0], acc0, acc1);
     else mfma_step<WT, MODE>(s.t[0], out, out);
-    interleave_step<NMFMA>();
     __syncthreads();
     // second half (tile t[1]): stage the next block's first half, fetch its second half
     stage_store<WT, MODE, 0>(st, s.t[0], s.blk[(kb + 1) & 1]);
@@ -440,25 +396,21 @@ __global__ void __launch_bounds__(GT, 1) gemm_kernel(const GemmArgs g) {
     } else {
       mfma_step<WT, MODE>(s.t[1], out, out);
     }
-    interleave_step<NMFMA>();
     if constexpr (MODE == GEMM_Q8K) block_end<WT>(s.blk[kb & 1], acc0, acc1, out);
     __syncthreads();
   }
 
   // epilogue: y[m][n] = out (+ resid[m][n])
+  const int n = n0 + 32 * wn + lr;
 #pragma unroll
   for (int i = 0; i < 2; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int n = n0 + 64 * wn + 32 * j + lr;
-#pragma unroll
-      for (int e = 0; e < 16; e++) {
-        const int m = m0 + 64 * wm + 32 * i + (e / 4) * 8 + (lane >> 5) * 4 + (e % 4);
-        if (m < g.M && n < g.N) {
-          float v = out[i][j][e];
-          if (g.resid) v = v + g.resid[(size_t)m * g.ldr + n];
-          g.y[(size_t)m * g.ldy + n] = v;
-        }
+    for (int e = 0; e < 16; e++) {
+      const int m = m0 + 64 * wm + 32 * i + (e / 4) * 8 + (lane >> 5) * 4 + (e % 4);
+      if (m < g.M && n < g.N) {
+        float v = out[i][e];
+        if (g.resid) v = v + g.resid[(size_t)m * g.ldr + n];
+        g.y[(size_t)m * g.ldy + n] = v;
       }
     }
 }
