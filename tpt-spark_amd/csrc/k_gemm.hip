@@ -43,14 +43,18 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int GT = 512;          // threads per workgroup
 constexpr int BM = 128, BN = 128, BK = 128;
-constexpr int LDK = BK + 2;      // fp16 per LDS row: a 4-byte pad spreads the MFMA operand reads over
-                                 // the banks (measured: 16 B of pad left 9x the bank-conflict cycles)
 constexpr int LDG = 16;          // per-16 sums / mins row
 
-struct GemmTile {                // one K step's operands
-  _Float16 a[BM][LDK];
-  _Float16 b[BN][LDK];
+// One K step's operands, rows of BK fp16 (256 B) without padding: the 16-byte chunk c of row r
+// sits at chunk position c ^ (r % 16), so that the 16 rows one MFMA operand read touches per
+// chunk column spread over all banks, and every operand read and staging write is one aligned
+// 16-byte LDS access.
+struct GemmTile {
+  __attribute__((aligned(16))) _Float16 a[BM * BK];
+  __attribute__((aligned(16))) _Float16 b[BN * BK];
 };
+// element index of (row r, column k) in a tile, k a multiple of 8
+__device__ __forceinline__ int sw(int r, int k) { return r * BK + ((((k >> 3) ^ (r & 15))) << 3); }
 struct GemmBlock {               // GEMM_Q8K: one super-block's per-row and per-column data
   _Float16 a16[BM][LDG];         // activation per-16 sums
   _Float16 b16[BN][LDG];         // weight mins, each repeated for its two 16-element halves
@@ -144,7 +148,7 @@ template <int WT, int MODE, int HB>
 __device__ __forceinline__ void stage_store(const Stage<WT>& st, GemmTile& T, GemmBlock& B) {
   const int tid = threadIdx.x, r = tid >> 2, qt = tid & 3;
 #pragma unroll
-  for (int i = 0; i < 4; i++) *(u32x4*)&T.a[r][32 * qt + 8 * i] = st.a[i];
+  for (int i = 0; i < 4; i++) *(u32x4*)&T.a[sw(r, 32 * qt + 8 * i)] = st.a[i];
   float d, dmin = 0.f;
   if constexpr (WT == TPT_TYPE_Q4_K) {
     // weight row r, group g = 2 HB + qt / 2: qs[32g + l] holds element 64g + l (low nibble,
@@ -180,8 +184,8 @@ __device__ __forceinline__ void stage_store(const Stage<WT>& st, GemmTile& T, Ge
           hi[2 * h] = dec(p01 >> 4, s1);
           hi[2 * h + 1] = dec(p23 >> 4, s1);
         }
-        *(u32x4*)&T.b[r][c0 + 8 * c] = lo;
-        *(u32x4*)&T.b[r][c0 + 32 + 8 * c] = hi;
+        *(u32x4*)&T.b[sw(r, c0 + 8 * c)] = lo;
+        *(u32x4*)&T.b[sw(r, c0 + 32 + 8 * c)] = hi;
       }
       // mins of sub-blocks 2g, 2g + 1, each for its two 16-element halves (16-sums 8g .. 8g+3)
       const half2 mm0 = {(_Float16)m0, (_Float16)m0}, mm1 = {(_Float16)m1, (_Float16)m1};
@@ -207,8 +211,8 @@ __device__ __forceinline__ void stage_store(const Stage<WT>& st, GemmTile& T, Ge
           lo[t] = (_Float16)(d1 * (float)(byte & 0xF) - mm1);
           hi[t] = (_Float16)(d2 * (float)(byte >> 4) - mm2);
         }
-        *(half8*)&T.b[r][c0 + 8 * c] = lo;
-        *(half8*)&T.b[r][c0 + 32 + 8 * c] = hi;
+        *(half8*)&T.b[sw(r, c0 + 8 * c)] = lo;
+        *(half8*)&T.b[sw(r, c0 + 32 + 8 * c)] = hi;
       }
     }
   } else {
@@ -245,13 +249,13 @@ __device__ __forceinline__ void stage_store(const Stage<WT>& st, GemmTile& T, Ge
           o[2 * h] = ((w01 << 2) & 0xFF00FF00u) | (w01 & 0x003F003Fu);
           o[2 * h + 1] = ((w23 << 2) & 0xFF00FF00u) | (w23 & 0x003F003Fu);
         }
-        *(u32x4*)&T.b[r][32 * qt + 8 * c] = o;
+        *(u32x4*)&T.b[sw(r, 32 * qt + 8 * c)] = o;
       } else {
         const float ds = d * (float)s;
         half8 v;
 #pragma unroll
         for (int t = 0; t < 8; t++) v[t] = (_Float16)(ds * (float)((int)((qv[t / 4] >> (8 * (t % 4))) & 0xff) - 32));
-        *(half8*)&T.b[r][32 * qt + 8 * c] = v;
+        *(half8*)&T.b[sw(r, 32 * qt + 8 * c)] = v;
       }
     }
   }
@@ -276,9 +280,9 @@ __device__ __forceinline__ void mfma_step(const GemmTile& T, floatx16 (&acc)[2],
   for (int kk = 0; kk < BK; kk += 16) {
     half8 a[2];
 #pragma unroll
-    for (int i = 0; i < 2; i++) a[i] = *(const half8*)&T.a[64 * wm + 32 * i + lr][kk + lk];
+    for (int i = 0; i < 2; i++) a[i] = *(const half8*)&T.a[sw(64 * wm + 32 * i + lr, kk + lk)];
     if constexpr (WT == TPT_TYPE_Q6_K && MODE == GEMM_Q8K) {
-      const u32x4 raw = *(const u32x4*)&T.b[32 * wn + lr][kk + lk];
+      const u32x4 raw = *(const u32x4*)&T.b[sw(32 * wn + lr, kk + lk)];
       const half2 k1088 = {(_Float16)1088.f, (_Float16)1088.f}, k1024 = {(_Float16)1024.f, (_Float16)1024.f};
       u32x4 h, l;
 #pragma unroll
@@ -293,7 +297,7 @@ __device__ __forceinline__ void mfma_step(const GemmTile& T, floatx16 (&acc)[2],
         lo[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bl, lo[i], 0, 0, 0);
       }
     } else {
-      const half8 b = *(const half8*)&T.b[32 * wn + lr][kk + lk];
+      const half8 b = *(const half8*)&T.b[sw(32 * wn + lr, kk + lk)];
 #pragma unroll
       for (int i = 0; i < 2; i++) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b, acc[i], 0, 0, 0);
     }
