@@ -62,7 +62,7 @@ struct tpt_model {
   int dec_check();                 // reports a timed-out barrier wait, then clears the state
 
   // batched prefill (MFMA GEMMs over up to kPrefillT positions at once)
-  static constexpr int kPrefillT = 1024;
+  static constexpr int kPrefillT = 2048;
   bool batched_prefill = false;       // every layer matrix is Q4_K
   bool causal_mfma = true;            // prompt attention on the matrix cores where supported
   void* pf_mem = nullptr;             // scratch of the batched prefill, grown on demand
