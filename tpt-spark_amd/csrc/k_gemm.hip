@@ -163,13 +163,15 @@ __device__ __forceinline__ void stage_store(const Stage<WT>& st, GemmTile& T, Ge
     get_scale_min(st.h, 2 * g + 1, &sc1, &m1);
     if constexpr (MODE == GEMM_Q8K) {
       // the integers sc * q two at a time in packed fp16, all exact: a byte pair (b, b') moved
-      // to the two halves, its nibbles ORed into the mantissa of 1024.0 (0x6400) give 1024 + q,
-      // minus 1024 gives q, times sc gives sc * q <= 945 < 2048
+      // to the two halves, its nibbles ORed into the mantissa of 1024.0 (0x6400) give 1024 + q;
+      // one fused multiply-add (1024 + q) * sc - 1024 sc rounds once, onto the integer
+      // sc * q <= 945 < 2048 (1024 sc <= 64512 is exact in fp16)
       const half2 s0 = {(_Float16)sc0, (_Float16)sc0}, s1 = {(_Float16)sc1, (_Float16)sc1};
-      const half2 k1024 = {(_Float16)1024.f, (_Float16)1024.f};
-      auto dec = [&](uint32_t pair, half2 sc) {
-        const half2 v = __builtin_bit_cast(half2, (pair & 0x000F000Fu) | 0x64006400u) - k1024;
-        return __builtin_bit_cast(uint32_t, v * sc);
+      const half2 o0 = {(_Float16)(-1024 * sc0), (_Float16)(-1024 * sc0)};
+      const half2 o1 = {(_Float16)(-1024 * sc1), (_Float16)(-1024 * sc1)};
+      auto dec = [&](uint32_t pair, half2 sc, half2 off) {
+        const half2 v = __builtin_bit_cast(half2, (pair & 0x000F000Fu) | 0x64006400u);
+        return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(v, sc, off));
       };
 #pragma unroll
       for (int c = 0; c < 2; c++) {  // 8 consecutive elements per 16-byte store
@@ -179,10 +181,10 @@ __device__ __forceinline__ void stage_store(const Stage<WT>& st, GemmTile& T, Ge
           const uint32_t x = st.q[2 * c + h];
           const uint32_t p01 = __builtin_amdgcn_perm(0u, x, 0x0c010c00u);  // bytes 0, 1 -> halves
           const uint32_t p23 = __builtin_amdgcn_perm(0u, x, 0x0c030c02u);  // bytes 2, 3 -> halves
-          lo[2 * h] = dec(p01, s0);
-          lo[2 * h + 1] = dec(p23, s0);
-          hi[2 * h] = dec(p01 >> 4, s1);
-          hi[2 * h + 1] = dec(p23 >> 4, s1);
+          lo[2 * h] = dec(p01, s0, o0);
+          lo[2 * h + 1] = dec(p23, s0, o0);
+          hi[2 * h] = dec(p01 >> 4, s1, o1);
+          hi[2 * h + 1] = dec(p23 >> 4, s1, o1);
         }
         *(u32x4*)&T.b[sw(r, c0 + 8 * c)] = lo;
         *(u32x4*)&T.b[sw(r, c0 + 32 + 8 * c)] = hi;
@@ -304,10 +306,11 @@ __device__ __forceinline__ void mfma_step(const GemmTile& T, floatx16 (&acc)[2],
   }
 }
 
-// GEMM_Q8K end of a super-block, per element in f32 as candle (y += d * (float)isum with
-// d = d_w * d_x).  Q4_K: isum = the two exact 128-element chains added once, and the mins term
-// sum_j m_j * bsum_j on the matrix cores (K = 16, exact) enters as - (dmin_w d_x) msum.  Q6_K:
-// isum = 64 hi + lo (64 hi exact, one rounding); no mins term.
+// GEMM_Q8K end of a super-block, per element in f32: candle's y += d_x (d_w isum - dmin_w msum)
+// with the integers exact (the same terms as candle's (d_w d_x) isum - (dmin_w d_x) msum; the
+// f32 roundings differ by an ulp).  Q4_K: isum = the two exact 128-element chains added once,
+// the mins term sum_j m_j * bsum_j on the matrix cores (K = 16, exact); per element one add and
+// three (fused) multiplies.  Q6_K: isum = 64 hi + lo (64 hi exact, one rounding); no mins term.
 template <int WT>
 __device__ __forceinline__ void block_end(const GemmBlock& B, floatx16 (&acc0)[2], floatx16 (&acc1)[2],
                                           floatx16 (&out)[2]) {
@@ -336,17 +339,15 @@ __device__ __forceinline__ void block_end(const GemmBlock& B, floatx16 (&acc0)[2
       const floatx16 accm = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, floatx16{}, 0, 0, 0);
 #pragma unroll
       for (int e = 0; e < 16; e++) {
-        const float dx = dxs[e];
         const float isum = acc0[i][e] + acc1[i][e];
-        const float dd = dw * dx, ddm = dm * dx;
-        const float v = dd * isum - ddm * accm[e];
-        out[i][e] = out[i][e] + v;
+        const float t = fmaf(dw, isum, -(dm * accm[e]));
+        out[i][e] = fmaf(dxs[e], t, out[i][e]);
       }
     } else {
 #pragma unroll
       for (int e = 0; e < 16; e++) {
         const float isum = fmaf(64.f, acc0[i][e], acc1[i][e]);
-        out[i][e] = out[i][e] + (dw * dxs[e]) * isum;
+        out[i][e] = fmaf(dxs[e], dw * isum, out[i][e]);
       }
     }
     acc0[i] = floatx16{};
