@@ -118,9 +118,9 @@ def attn_roofline(tp, ctx, iters=64):
     return out
 
 
-# causal prompt attention: (Nq, Nkv, hd, L0 cached positions, T queries) -- the two 1024-query
-# slices of the 2048-token prompt at the Llama-3 8B head shape
-ATTN_CAUSAL_CASES = [(32, 8, 128, 0, 1024), (32, 8, 128, 1024, 1024)]
+# causal prompt attention: (Nq, Nkv, hd, L0 cached positions, T queries) at the Llama-3 8B head
+# shape -- the 2048-token prompt (one slice), and the second slice of a 4096-token prompt
+ATTN_CAUSAL_CASES = [(32, 8, 128, 0, 2048), (32, 8, 128, 2048, 2048)]
 
 
 def attn_causal_roofline(tp, ctx, iters=20):

@@ -16,8 +16,8 @@
 // toward zero, lo = q - hi rounded toward zero: |q - hi - lo| < 2^-20 |q|), and every product is
 // two MFMAs (hi, lo) accumulated in f32.  Per 32-key block and wave:
 //   S^T[key][query] = K . (q * scale * log2 e)^T   (A = K rows from LDS, B = q pairs in registers)
-//   p = exp2(S^T - m), m the running max of the query's scores (one lane per query: each lane
-//       holds 16 of a query's 32 scores, the other half-wave the other 16)
+//   p = exp2(S^T - m), m the running max of the query's scores up to a slack of 8 (one lane per
+//       query: each lane holds 16 of a query's 32 scores, the other half-wave the other 16)
 //   O^T[d][query] = O^T * exp2(m_old - m) + V^T . P^T   (A = V^T from LDS, B = the p pairs)
 // The score tile's register layout is used directly as the B operand of the second product: the
 // 16-key reduction slots of a lane are its own 8 scores of the step, and the V^T rows are read in
@@ -39,13 +39,18 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int QB = 32;  // query positions per workgroup (the MFMA N of both products)
 constexpr int KB = 32;  // keys per block (the MFMA M of the score tile)
 
-// (x0, x1) -> packed fp16 hi and lo words with hi + lo = x to 2^-20 relative
+// (x0, x1) -> packed fp16 hi and lo words with hi + lo = x to 2^-20 relative (the remainders
+// x - hi are exact: mixed-precision fused multiply-adds on the fp16 hi)
 __device__ __forceinline__ void split_pair(float x0, float x1, uint32_t& hi, uint32_t& lo) {
   const auto h = __builtin_amdgcn_cvt_pkrtz(x0, x1);
-  const float r0 = x0 - (float)h[0], r1 = x1 - (float)h[1];
+  const float r0 = __builtin_fmaf((float)h[0], -1.f, x0), r1 = __builtin_fmaf((float)h[1], -1.f, x1);
   hi = __builtin_bit_cast(uint32_t, h);
   lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(r0, r1));
 }
+
+// Slack of the running max (log2 units): the max moves only when a block's scores pass it by
+// more than this, so the output rescale is rare; p = 2^(s - m) then stays below 2^8.
+constexpr float MAX_SLACK = 8.f;
 
 template <int HD, int G>
 __global__ void __launch_bounds__(64 * G) attn_causal_kernel(const AttnArgs a, const float qscale) {
@@ -177,13 +182,16 @@ __global__ void __launch_bounds__(64 * G) attn_causal_kernel(const AttnArgs a, c
 #pragma unroll
     for (int e = 1; e < 16; e++) mx = fmaxf(mx, sacc[e]);
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mnew = fmaxf(m, mx);  // finite: key 0 is visible to every query
-    const float alpha = exp2f(m - mnew);
+    // finite after the first block: key 0 is visible to every query
+    const float mnew = mx > m + MAX_SLACK ? mx : m;
+    // 2^(m - mnew) and 2^(s - mnew) on v_exp_f32 directly: the arguments are <= 8, and results
+    // below 2^-126 (flushed or not) are negligible against the running sum
+    const float alpha = __builtin_amdgcn_exp2f(m - mnew);
     m = mnew;
     float ps = 0.f;
 #pragma unroll
     for (int e = 0; e < 16; e++) {
-      sacc[e] = exp2f(sacc[e] - mnew);
+      sacc[e] = __builtin_amdgcn_exp2f(sacc[e] - mnew);
       ps += sacc[e];
     }
     l = l * alpha + ps;
