@@ -53,7 +53,7 @@ __device__ __forceinline__ void split_pair(float x0, float x1, uint32_t& hi, uin
 constexpr float MAX_SLACK = 8.f;
 
 template <int HD, int G>
-__global__ void __launch_bounds__(64 * G) attn_causal_kernel(const AttnArgs a, const float qscale) {
+__global__ void __launch_bounds__(64 * G, 2) attn_causal_kernel(const AttnArgs a, const float qscale) {
   constexpr int NT = 64 * G;
   constexpr int KS = HD / 16;                // 16-dim steps of the score product
   constexpr int OT = HD / 32;                // 32-dim tiles of the output
