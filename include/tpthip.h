@@ -34,12 +34,14 @@ extern "C" {
 /* ggml tensor types the path reads (values are ggml's GGML_TYPE_* numbers) */
 #define TPT_TYPE_F32 0
 #define TPT_TYPE_F16 1
+#define TPT_TYPE_Q4_0 2
 #define TPT_TYPE_Q8_0 8
 #define TPT_TYPE_Q4_K 12
+#define TPT_TYPE_Q5_K 13
 #define TPT_TYPE_Q6_K 14
 
 /* activation handling of a GEMV.  TPT_ACT_Q8: the fp32 input is quantized the way candle's
- * QMatMul does on the CPU (Q8_K per 256 for k-quant weights, Q8_0 per 32 for Q8_0 weights)
+ * QMatMul does on the CPU (Q8_K per 256 for k-quant weights, Q8_0 per 32 for Q8_0 and Q4_0)
  * and dotted in integer arithmetic -- the parity path.  TPT_ACT_F32: dequantized weights
  * times fp32 activations, fp32 accumulate. */
 #define TPT_ACT_Q8 0
@@ -69,10 +71,11 @@ int tpt_memcpy_d2h(tpt_ctx* ctx, void* dst, const void* src, size_t bytes);
 int tpt_memset(tpt_ctx* ctx, void* dst, int value, size_t bytes);
 
 /* ------------------------------------------------------------------ op level */
-/* Bit-exact k-quant dequantization of n elements to fp32.  Replaces the dequant_* WGSL
- * shaders (src-tauri/src/engine/shaders/dequant_q4k.wgsl:74-115, dequant_q6k.wgsl:58-92,
- * dequant_q8.wgsl:51-73) as dispatched by append_dequant (wgpu_engine.rs:551-570), with
- * ggml's Q4_K element order (the WGSL Q4_K order is not ggml's). */
+/* Bit-exact dequantization of n elements to fp32 (Q4_K, Q5_K, Q6_K, Q8_0, Q4_0, F16, F32).
+ * Replaces the dequant_* WGSL shaders (src-tauri/src/engine/shaders/dequant_q4k.wgsl:74-115,
+ * dequant_q5k.wgsl:78-104, dequant_q6k.wgsl:58-92, dequant_q8.wgsl:51-73) as dispatched by
+ * append_dequant (wgpu_engine.rs:551-570), with ggml's Q4_K and Q5_K element orders (the
+ * WGSL ones are not ggml's). */
 int tpt_dequant(tpt_ctx* ctx, int type, const void* w, float* y, int64_t n);
 
 /* y[N] = W[N,K] . x[K] with W in GGUF block layout, rows contiguous.  Replaces

@@ -67,7 +67,9 @@ size_t orc_type_size(int t) {
     case ORC_F16: return 2;
     case ORC_Q8_0: return sizeof(orc_blk_q8_0);
     case ORC_Q4_K: return sizeof(orc_blk_q4k);
+    case ORC_Q5_K: return sizeof(orc_blk_q5k);
     case ORC_Q6_K: return sizeof(orc_blk_q6k);
+    case ORC_Q4_0: return sizeof(orc_blk_q4_0);
     case ORC_Q8_K: return sizeof(orc_blk_q8k);
   }
   return 0;
@@ -76,8 +78,8 @@ size_t orc_type_size(int t) {
 int orc_block_size(int t) {
   switch (t) {
     case ORC_F32: case ORC_F16: return 1;
-    case ORC_Q8_0: return ORC_QK8_0;
-    case ORC_Q4_K: case ORC_Q6_K: case ORC_Q8_K: return ORC_QK_K;
+    case ORC_Q8_0: case ORC_Q4_0: return ORC_QK8_0;
+    case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: case ORC_Q8_K: return ORC_QK_K;
   }
   return 0;
 }
@@ -115,6 +117,45 @@ static void dequant_q4k(const orc_blk_q4k* x, float* y, int64_t nb) {
       q += 32;
       is += 2;
     }
+  }
+}
+
+/* candle BlockQ5K::to_float (ggml dequantize_row_q5_K): Q4_K's layout and scales plus a fifth
+ * bit per element from qh: for the j-th 64-element group, bit 2j of qh[l] goes to element l of
+ * the low-nibble half and bit 2j+1 to element l of the high-nibble half. */
+static void dequant_q5k(const orc_blk_q5k* x, float* y, int64_t nb) {
+  for (int64_t i = 0; i < nb; i++) {
+    const float d = orc_fp16_to_f32(x[i].d), min = orc_fp16_to_f32(x[i].dmin);
+    const uint8_t* ql = x[i].qs;
+    const uint8_t* qh = x[i].qh;
+    int is = 0;
+    uint8_t u1 = 1, u2 = 2;
+    for (int j = 0; j < ORC_QK_K; j += 64) {
+      uint8_t sc, m;
+      scale_min_k4(is + 0, x[i].scales, &sc, &m);
+      const float d1 = d * sc, m1 = min * m;
+      scale_min_k4(is + 1, x[i].scales, &sc, &m);
+      const float d2 = d * sc, m2 = min * m;
+      for (int l = 0; l < 32; l++) *y++ = d1 * ((ql[l] & 0xF) + (qh[l] & u1 ? 16 : 0)) - m1;
+      for (int l = 0; l < 32; l++) *y++ = d2 * ((ql[l] >> 4) + (qh[l] & u2 ? 16 : 0)) - m2;
+      ql += 32;
+      is += 2;
+      u1 <<= 2;
+      u2 <<= 2;
+    }
+  }
+}
+
+/* candle BlockQ4_0::to_float (ggml dequantize_row_q4_0): element j < 16 is the low nibble of
+ * qs[j], element j + 16 its high nibble, each minus 8, times d */
+static void dequant_q4_0(const orc_blk_q4_0* x, float* y, int64_t nb) {
+  for (int64_t i = 0; i < nb; i++) {
+    const float d = orc_fp16_to_f32(x[i].d);
+    for (int j = 0; j < 16; j++) {
+      y[j] = (float)((x[i].qs[j] & 0xF) - 8) * d;
+      y[j + 16] = (float)((x[i].qs[j] >> 4) - 8) * d;
+    }
+    y += 32;
   }
 }
 
@@ -163,6 +204,8 @@ int orc_dequant(int type, const void* src, float* dst, int64_t n) {
       for (int64_t i = 0; i < n; i++) dst[i] = orc_fp16_to_f32(((const uint16_t*)src)[i]);
       return 0;
     case ORC_Q4_K: dequant_q4k((const orc_blk_q4k*)src, dst, n / bs); return 0;
+    case ORC_Q5_K: dequant_q5k((const orc_blk_q5k*)src, dst, n / bs); return 0;
+    case ORC_Q4_0: dequant_q4_0((const orc_blk_q4_0*)src, dst, n / bs); return 0;
     case ORC_Q6_K: dequant_q6k((const orc_blk_q6k*)src, dst, n / bs); return 0;
     case ORC_Q8_0: dequant_q8_0((const orc_blk_q8_0*)src, dst, n / bs); return 0;
     case ORC_Q8_K: {
@@ -293,6 +336,77 @@ static float vec_dot_q4k_q8k(int64_t n, const orc_blk_q4k* x, const orc_blk_q8k*
   return sumf + s;
 }
 
+/* candle BlockQ5K::vec_dot_unopt (ggml generic ggml_vec_dot_q5_K_q8_K): vec_dot_q4k_q8k with
+ * the 5-bit values (nibble + 16 * qh bit). */
+static float vec_dot_q5k_q8k(int64_t n, const orc_blk_q5k* x, const orc_blk_q8k* y) {
+  int8_t aux8[ORC_QK_K];
+  int16_t aux16[8];
+  float sums[8] = {0};
+  int32_t aux32[8];
+  float sumf = 0.f;
+  for (int64_t i = 0; i < n / ORC_QK_K; i++) {
+    const uint8_t* q4 = x[i].qs;
+    const uint8_t* hm = x[i].qh;
+    const int8_t* q8 = y[i].qs;
+    memset(aux32, 0, sizeof(aux32));
+    int8_t* a = aux8;
+    uint8_t m = 1;
+    for (int j = 0; j < ORC_QK_K / 64; j++) {
+      for (int l = 0; l < 32; l++) a[l] = (int8_t)(q4[l] & 0xF);
+      for (int l = 0; l < 32; l++) a[l] += (hm[l] & m ? 16 : 0);
+      a += 32;
+      m <<= 1;
+      for (int l = 0; l < 32; l++) a[l] = (int8_t)(q4[l] >> 4);
+      for (int l = 0; l < 32; l++) a[l] += (hm[l] & m ? 16 : 0);
+      a += 32;
+      m <<= 1;
+      q4 += 32;
+    }
+    uint8_t scales[8], mins[8];
+    for (int j = 0; j < 8; j++) scale_min_k4(j, x[i].scales, &scales[j], &mins[j]);
+    int sumi = 0;
+    for (int j = 0; j < ORC_QK_K / 16; j++) sumi += y[i].bsums[j] * mins[j / 2];
+    a = aux8;
+    for (int j = 0; j < 8; j++) {
+      int32_t scale = scales[j];
+      for (int r = 0; r < 4; r++) {
+        for (int l = 0; l < 8; l++) aux16[l] = (int16_t)(q8[l] * a[l]);
+        for (int l = 0; l < 8; l++) aux32[l] += scale * aux16[l];
+        q8 += 8;
+        a += 8;
+      }
+    }
+    const float d = orc_fp16_to_f32(x[i].d) * y[i].d;
+    const float dmin = orc_fp16_to_f32(x[i].dmin) * y[i].d;
+    if (g_dot_block_order) {
+      int32_t t = 0;
+      for (int l = 0; l < 8; l++) t += aux32[l];
+      sumf += d * (float)t - dmin * (float)sumi;
+      continue;
+    }
+    for (int l = 0; l < 8; l++) sums[l] += d * (float)aux32[l];
+    sumf -= dmin * (float)sumi;
+  }
+  float s = 0.f;
+  for (int l = 0; l < 8; l++) s += sums[l];
+  return sumf + s;
+}
+
+/* candle BlockQ4_0::vec_dot_unopt (ggml generic ggml_vec_dot_q4_0_q8_0): per 32-block
+ * sumi = sum (q_lo - 8) y[j] + (q_hi - 8) y[j + 16], sumf += (float)sumi * d_w * d_x */
+static float vec_dot_q4_0_q8_0(int64_t n, const orc_blk_q4_0* x, const orc_blk_q8_0* y) {
+  float sumf = 0.f;
+  for (int64_t i = 0; i < n / ORC_QK8_0; i++) {
+    int32_t s0 = 0, s1 = 0;
+    for (int j = 0; j < 16; j++) {
+      s0 += ((x[i].qs[j] & 0xF) - 8) * (int32_t)y[i].qs[j];
+      s1 += ((x[i].qs[j] >> 4) - 8) * (int32_t)y[i].qs[j + 16];
+    }
+    sumf += (float)(s0 + s1) * orc_fp16_to_f32(x[i].d) * orc_fp16_to_f32(y[i].d);
+  }
+  return sumf;
+}
+
 /* candle BlockQ6K::vec_dot_unopt (ggml generic ggml_vec_dot_q6_K_q8_K); the per-lane
  * accumulator is f32 there, which holds these integer partial sums exactly. */
 static float vec_dot_q6k_q8k(int64_t n, const orc_blk_q6k* x, const orc_blk_q8k* y) {
@@ -353,13 +467,17 @@ static float vec_dot_q8_0_q8_0(int64_t n, const orc_blk_q8_0* x, const orc_blk_q
 float orc_vec_dot(int type, int64_t k, const void* w_row, const void* act_q) {
   switch (type) {
     case ORC_Q4_K: return vec_dot_q4k_q8k(k, (const orc_blk_q4k*)w_row, (const orc_blk_q8k*)act_q);
+    case ORC_Q5_K: return vec_dot_q5k_q8k(k, (const orc_blk_q5k*)w_row, (const orc_blk_q8k*)act_q);
     case ORC_Q6_K: return vec_dot_q6k_q8k(k, (const orc_blk_q6k*)w_row, (const orc_blk_q8k*)act_q);
+    case ORC_Q4_0: return vec_dot_q4_0_q8_0(k, (const orc_blk_q4_0*)w_row, (const orc_blk_q8_0*)act_q);
     case ORC_Q8_0: return vec_dot_q8_0_q8_0(k, (const orc_blk_q8_0*)w_row, (const orc_blk_q8_0*)act_q);
   }
   return NAN;
 }
 
-static int is_quant_type(int t) { return t == ORC_Q4_K || t == ORC_Q6_K || t == ORC_Q8_0; }
+static int is_quant_type(int t) {
+  return t == ORC_Q4_K || t == ORC_Q5_K || t == ORC_Q6_K || t == ORC_Q8_0 || t == ORC_Q4_0;
+}
 
 /* candle k_quants::matmul: each lhs row is quantized to the weight type's VecDotType
  * (Q8_K for k-quants, Q8_0 for Q8_0), then one vec_dot per output column (rayon there,
@@ -384,7 +502,7 @@ int orc_matmul(int type, int64_t m, int64_t k, int64_t n, const float* lhs, cons
   const int bs = orc_block_size(type);
   if (k % bs) return -2;
   const size_t row_bytes = (size_t)(k / bs) * orc_type_size(type);
-  const int act_type = type == ORC_Q8_0 ? ORC_Q8_0 : ORC_Q8_K;
+  const int act_type = type == ORC_Q8_0 || type == ORC_Q4_0 ? ORC_Q8_0 : ORC_Q8_K;
   const size_t act_row = (size_t)(k / orc_block_size(act_type)) * orc_type_size(act_type);
   uint8_t* aq = (uint8_t*)malloc(act_row * (size_t)m);
   if (!aq) return -3;

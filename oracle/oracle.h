@@ -14,8 +14,10 @@
  *
  * Pinning status (what checks each function; see tests/test_oracle_golden.py):
  *   dequant q4k/q6k/q8_0      hand-built known-answer blocks + closed forms         PINNED
+ *   dequant q5k/q4_0          hand-built known-answer blocks (every 5th-bit lane,
+ *                             both nibbles, the -8 offset)                          PINNED
  *   quantize_q8k / q8_0       hand-computed known answers (tie rule, half-away)     PINNED
- *   vec_dot q4k/q6k/q8_0      fp64 identity over dequantized operands               PINNED
+ *   vec_dot q4k/q5k/q6k/q8_0/q4_0  fp64 identity over dequantized operands          PINNED
  *   rmsnorm / silu / rope     closed forms (constant vector, 0, pos=0, pair norm)   PINNED
  *   attention                 single position (o=v), uniform scores (o=mean V)      PINNED
  *   argmax                    crafted ties (last index wins), NaN order             PINNED
@@ -31,7 +33,7 @@
 extern "C" {
 #endif
 
-enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q6_K = 14, ORC_Q8_K = 15 };
+enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q5_K = 13, ORC_Q6_K = 14, ORC_Q8_K = 15 };
 
 #define ORC_QK_K 256
 #define ORC_QK8_0 32
@@ -40,6 +42,8 @@ enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q6_K = 14, ORC
 typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[128]; } orc_blk_q4k;      /* 144 B */
 typedef struct { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; } orc_blk_q6k; /* 210 B */
 typedef struct { uint16_t d; int8_t qs[32]; } orc_blk_q8_0;                                  /*  34 B */
+typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qh[32]; uint8_t qs[128]; } orc_blk_q5k; /* 176 B */
+typedef struct { uint16_t d; uint8_t qs[16]; } orc_blk_q4_0;                                  /*  18 B */
 typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } orc_blk_q8k;                 /* 292 B */
 #pragma pack(pop)
 

@@ -366,6 +366,31 @@ def test_mixed_q4k_q6k_prefill(ctx, mixed_gguf):
         m_s.close()
 
 
+@pytest.mark.parametrize("qtype", [tpthip.TYPE_Q5_K, tpthip.TYPE_Q4_0])
+def test_other_quant_types_match_oracle(ctx, tmp_path, qtype):
+    """A tiny model whose layer matrices are Q5_K or Q4_0 (token_embd / output Q6_K): the
+    GEMV decode path (these types prefill one position at a time) against the oracle, f32
+    cache: prompt logits within 1e-3 and the first 16 greedy tokens identical."""
+    path = str(tmp_path / f"tiny-{qtype}.gguf")
+    synth.write_llama(path, synth.TINY, seed=9, type_matrix=qtype)
+    om = oracle.Model(path)
+    try:
+        om.reset(64, kv_f16=False)
+        ref = om.forward(PROMPT, 0)
+        want = om.greedy(PROMPT, 16, kv_f16=False)[0]
+    finally:
+        om.close()
+    m = tpthip.Model(ctx, path, max_ctx=64, kv_type=tpthip.TYPE_F32)
+    try:
+        nxt, lg = m.prefill(PROMPT, 0, logits=True)
+        got = [nxt] + m.decode_greedy(nxt, len(PROMPT), 15)
+    finally:
+        m.close()
+    print(qtype, "logits max-abs vs oracle", float(np.abs(lg - ref).max()))
+    assert np.abs(lg - ref).max() < 1e-3
+    assert got == want
+
+
 @pytest.fixture(scope="module")
 def gguf_1b(tmp_path_factory):
     """Llama 1B shape (16 layers, hidden 2048, 32/8 heads, head_dim 64, FFN 8192, vocab 128256,

@@ -13,11 +13,11 @@ import pytest
 
 import oracle
 import tpthip
-from tpthip import synth, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0
+from tpthip import synth, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0, TYPE_Q4_0
 
 pytestmark = pytest.mark.gpu
 
-QTYPES = [TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0]
+QTYPES = [TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0, TYPE_Q4_0]
 
 
 def rel_l2(a, b):
@@ -32,7 +32,7 @@ def random_blocks(qtype, nblocks, seed):
     pool = np.array([0x0001, 0x03FF, 0x0400, 0x1000, 0x2400, 0x3C00, 0x5800, 0x7BFF, 0x8400, 0x9800],
                     np.uint16)
     h = rng.choice(pool, (nblocks, 2)).astype("<u2").view(np.uint8)
-    if qtype == TYPE_Q4_K:
+    if qtype in (TYPE_Q4_K, TYPE_Q5_K):
         raw[:, 0:4] = h.reshape(nblocks, 4)
     elif qtype == TYPE_Q6_K:
         raw[:, 208:210] = h[:, :2]
@@ -59,6 +59,19 @@ def test_dequant_known_answer_blocks(ctx):
     y = ctx.dequant(TYPE_Q4_K, ctx.to_device(np.frombuffer(blk, np.uint8)), 256)
     for k, v in g["expect"].items():
         assert y[int(k)] == v
+
+
+def test_dequant_hand_blocks_q5k_q4_0(ctx):
+    """The hand-worked Q5_K and Q4_0 blocks of the oracle's known-answer tests on the GPU
+    (embedding rows and tpt_dequant go through this element decode)."""
+    qs = bytes([(i % 16) | ((15 - i % 16) << 4) for i in range(128)])
+    qh = bytes([0xFF if l % 2 else 0 for l in range(32)])
+    q5 = struct.pack("<HH", 0x3C00, 0x3800) + bytes([1, 2, 3, 4, 0, 1, 2, 3, 0x21, 0x43, 0x65, 0x87]) + qh + qs
+    y = ctx.dequant(TYPE_Q5_K, ctx.to_device(np.frombuffer(q5, np.uint8)), 256)
+    assert [y[k] for k in (0, 1, 33, 34, 69, 167, 222, 255)] == [0.0, 17.0, 59.5, 25.5, 62.0, 70.0, 67.0, 108.0]
+    q4 = struct.pack("<H", 0x3800) + bytes([j | ((15 - j) << 4) for j in range(16)])
+    y = ctx.dequant(TYPE_Q4_0, ctx.to_device(np.frombuffer(q4, np.uint8)), 32)
+    assert list(y[[0, 8, 15, 16, 20, 31]]) == [-4.0, 0.0, 3.5, 3.5, 1.5, -4.0]
 
 
 GEMV_SHAPES = [(4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)]

@@ -83,6 +83,40 @@ def test_q8_0_known_answers():
     assert not y[5:].any()
 
 
+def q5k_block():
+    """d = 1, dmin = 0.5; scale bytes giving (sc, m) = (1,0) (2,1) (3,2) (4,3) for sub-blocks 0-3
+    (low 6 bits of bytes 0-3 / 4-7) and (1,2) (3,4) (5,6) (7,8) for 4-7 (nibbles of bytes
+    8-11); qs[i] = (i % 16) | (15 - i % 16) << 4; qh[l] = 0xFF for odd l, 0 for even l (the
+    fifth bit of every sub-block set exactly on odd l)."""
+    qs = bytes([(i % 16) | ((15 - i % 16) << 4) for i in range(128)])
+    qh = bytes([0xFF if l % 2 else 0 for l in range(32)])
+    return struct.pack("<HH", 0x3C00, 0x3800) + bytes([1, 2, 3, 4, 0, 1, 2, 3, 0x21, 0x43, 0x65, 0x87]) + qh + qs
+
+
+def test_q5k_known_answers():
+    """Element e: group j = e // 64, half e % 64 // 32, l = e % 32; q = nibble + 16 * (l odd);
+    y = sc * q - 0.5 * m, worked by hand."""
+    y = oracle.dequant(oracle.Q5_K, np.frombuffer(q5k_block(), np.uint8), 256)
+    expect = {0: 0.0,      # j0 low, l0: nibble 0, bit clear, sc 1, m 0
+              1: 17.0,     # j0 low, l1: 1 + 16
+              33: 59.5,    # j0 high, l1: 14 + 16 = 30, sc 2: 60 - 0.5 * 1
+              34: 25.5,    # j0 high, l2: 13, sc 2: 26 - 0.5
+              69: 62.0,    # j1 low, l5: 5 + 16 = 21, sc 3: 63 - 0.5 * 2
+              167: 70.0,   # j2 high, l7: qs[71] high nibble 8 + 16 = 24, sc 3: 72 - 0.5 * 4
+              222: 67.0,   # j3 low, l30: 14, sc 5: 70 - 0.5 * 6
+              255: 108.0}  # j3 high, l31: 0 + 16, sc 7: 112 - 0.5 * 8
+    for k, v in expect.items():
+        assert y[k] == v, (k, y[k], v)
+
+
+def test_q4_0_known_answers():
+    """d = 0.5, qs[j] = j | (15 - j) << 4: element j < 16 is (j - 8) / 2, element j + 16 is
+    (7 - j) / 2."""
+    blk = struct.pack("<H", 0x3800) + bytes([j | ((15 - j) << 4) for j in range(16)])
+    y = oracle.dequant(oracle.Q4_0, np.frombuffer(blk, np.uint8), 32)
+    assert list(y[[0, 8, 15, 16, 20, 31]]) == [-4.0, 0.0, 3.5, 3.5, 1.5, -4.0]
+
+
 def q8k_parse(raw):
     d = struct.unpack("<f", raw[:4].tobytes())[0]
     return d, raw[4:260].view(np.int8), raw[260:292].view(np.int16)
@@ -129,7 +163,7 @@ def _rand_blocks(qtype, nblocks, seed):
     raw = rng.integers(0, 256, nblocks * oracle.TYPE_SIZE[qtype], dtype=np.uint8)
     blk = raw.reshape(nblocks, oracle.TYPE_SIZE[qtype])
     h = rng.integers(0x1000, 0x2400, (nblocks, 2)).astype("<u2").view(np.uint8)
-    if qtype == oracle.Q4_K:
+    if qtype in (oracle.Q4_K, oracle.Q5_K):
         blk[:, 0:4] = h.reshape(nblocks, 4)
     elif qtype == oracle.Q6_K:
         blk[:, 208:210] = h[:, :2]
@@ -138,14 +172,15 @@ def _rand_blocks(qtype, nblocks, seed):
     return raw
 
 
-@pytest.mark.parametrize("qtype", [oracle.Q4_K, oracle.Q6_K, oracle.Q8_0])
+@pytest.mark.parametrize("qtype", [oracle.Q4_K, oracle.Q5_K, oracle.Q6_K, oracle.Q8_0, oracle.Q4_0])
 def test_vec_dot_identity(qtype):
     """candle's integer vec_dot equals the fp64 dot of the two dequantized operands."""
     k, n = 1024, 24
     w = _rand_blocks(qtype, k // oracle.BLOCK[qtype] * n, 11)
     x = np.random.default_rng(3).standard_normal(k).astype(np.float32)
-    aq = oracle.quantize_q8_0(x) if qtype == oracle.Q8_0 else oracle.quantize_q8k(x)
-    xd = oracle.dequant(oracle.Q8_0 if qtype == oracle.Q8_0 else oracle.Q8_K, aq, k).astype(np.float64)
+    q80 = qtype in (oracle.Q8_0, oracle.Q4_0)
+    aq = oracle.quantize_q8_0(x) if q80 else oracle.quantize_q8k(x)
+    xd = oracle.dequant(oracle.Q8_0 if q80 else oracle.Q8_K, aq, k).astype(np.float64)
     rb = oracle.row_bytes(qtype, k)
     for r in range(n):
         wd = oracle.dequant(qtype, w[r * rb:(r + 1) * rb], k).astype(np.float64)

@@ -25,6 +25,11 @@ template <int WT> struct Raw;
 template <> struct Raw<TPT_TYPE_Q4_K> { uint4 h, a, b; };
 template <> struct Raw<TPT_TYPE_Q6_K> { uint4 qa, qb, qh; uint2 sc; uint32_t d; };
 template <> struct Raw<TPT_TYPE_Q8_0> { uint4 a0, a1, b0, b1; uint32_t d0, d1; };
+template <> struct Raw<TPT_TYPE_Q5_K> { uint4 h, a, b, ha, hb; };
+template <> struct Raw<TPT_TYPE_Q4_0> { uint4 a, b; uint32_t d0, d1; };
+
+// activation type of a weight type: Q8_0 rows for Q8_0 and Q4_0 weights, Q8_K for the k-quants
+template <int WT> constexpr bool act_q80() { return WT == TPT_TYPE_Q8_0 || WT == TPT_TYPE_Q4_0; }
 
 template <int WT>
 __device__ __forceinline__ void load_raw(const uint8_t* row, int g, Raw<WT>& r);
@@ -61,6 +66,27 @@ __device__ __forceinline__ void load_raw<TPT_TYPE_Q8_0>(const uint8_t* row, int 
   r.d1 = ldg_u<uint16_t>(b0 + 34);
   r.b0 = ldg_u<uint4>(b0 + 36);
   r.b1 = ldg_u<uint4>(b0 + 52);
+}
+
+template <>
+__device__ __forceinline__ void load_raw<TPT_TYPE_Q5_K>(const uint8_t* row, int g,
+                                                         Raw<TPT_TYPE_Q5_K>& r) {
+  const uint8_t* blk = row + (size_t)(g >> 2) * 176;  // 176 = 11 x 16: blocks stay 16-aligned
+  r.h = *(const uint4*)blk;
+  r.ha = *(const uint4*)(blk + 16);  // qh: the fifth bits of all four groups
+  r.hb = *(const uint4*)(blk + 32);
+  r.a = *(const uint4*)(blk + 48 + (g & 3) * 32);
+  r.b = *(const uint4*)(blk + 64 + (g & 3) * 32);
+}
+
+template <>
+__device__ __forceinline__ void load_raw<TPT_TYPE_Q4_0>(const uint8_t* row, int g,
+                                                         Raw<TPT_TYPE_Q4_0>& r) {
+  const uint8_t* b0 = row + (size_t)g * 36;  // blocks 2g, 2g + 1 (18 bytes: 2-byte aligned)
+  r.d0 = ldg_u<uint16_t>(b0);
+  r.a = ldg_u<uint4>(b0 + 2);
+  r.d1 = ldg_u<uint16_t>(b0 + 18);
+  r.b = ldg_u<uint4>(b0 + 20);
 }
 
 // ----------------------------------------------------------------- activation (LDS)
@@ -300,7 +326,7 @@ struct Act {
 
 template <int WT>
 __device__ __forceinline__ void load_act(const Lds& L, int g, Act& a) {
-  if constexpr (WT == TPT_TYPE_Q4_K) {
+  if constexpr (WT == TPT_TYPE_Q4_K || WT == TPT_TYPE_Q5_K) {
     const int4* q = (const int4*)(L.q32 + 16 * g);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -363,6 +389,55 @@ __device__ __forceinline__ float dot_group(const Raw<TPT_TYPE_Q4_K>& r, const Ac
   const float dd = h2f((uint16_t)(r.h.x & 0xffff)) * a.d0;
   const float dm = h2f((uint16_t)(r.h.x >> 16)) * a.d0;
   return dd * (float)isum - dm * (float)msum;
+}
+
+// Q5_K x Q8_K for one group: vec_dot_q5k_q8k's per-block arithmetic restricted to the group's
+// two sub-blocks -- Q4_K's with the values nibble + 16 * (bit 2(g%4) or 2(g%4)+1 of qh[l]).
+__device__ __forceinline__ float dot_group(const Raw<TPT_TYPE_Q5_K>& r, const Act& a, int g) {
+  const int sh = 16 * (g & 1);
+  const uint32_t Y = r.h.y >> sh, Z = r.h.z >> sh, W = r.h.w >> sh;
+  const bool hi = (g & 2) != 0;
+  const int sc0 = hi ? (int)((W & 0xF) | (((Y >> 6) & 3) << 4)) : (int)(Y & 63);
+  const int sc1 = hi ? (int)(((W >> 8) & 0xF) | (((Y >> 14) & 3) << 4)) : (int)((Y >> 8) & 63);
+  const int m0 = hi ? (int)(((W >> 4) & 0xF) | (((Z >> 6) & 3) << 4)) : (int)(Z & 63);
+  const int m1 = hi ? (int)(((W >> 12) & 0xF) | (((Z >> 14) & 3) << 4)) : (int)((Z >> 8) & 63);
+  const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+  const uint32_t qh[8] = {r.ha.x, r.ha.y, r.ha.z, r.ha.w, r.hb.x, r.hb.y, r.hb.z, r.hb.w};
+  const int b0 = 2 * (g & 3);
+  int s0 = 0, s1 = 0;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const uint32_t v0 = (w[i] & 0x0F0F0F0Fu) | (((qh[i] >> b0) & 0x01010101u) << 4);
+    const uint32_t v1 = ((w[i] >> 4) & 0x0F0F0F0Fu) | (((qh[i] >> (b0 + 1)) & 0x01010101u) << 4);
+    s0 = sdot4((int)v0, a.q[i], s0);
+    s1 = sdot4((int)v1, a.q[8 + i], s1);
+  }
+  // 6-bit scales times sums of at most 32 products of 5-bit and 8-bit values: exact in 24 bits
+  const int isum = __mul24(sc0, s0) + __mul24(sc1, s1);
+  const int msum = __mul24(m0, a.s[0]) + __mul24(m1, a.s[1]);
+  const float dd = h2f((uint16_t)(r.h.x & 0xffff)) * a.d0;
+  const float dm = h2f((uint16_t)(r.h.x >> 16)) * a.d0;
+  return dd * (float)isum - dm * (float)msum;
+}
+
+// Q4_0 x Q8_0 for two blocks: vec_dot_q4_0_q8_0's (float)sumi * d_w * d_x per block, with
+// sumi = sum (q - 8) y = sum q y - 8 sum y (the activation sums by dot products with ones).
+__device__ __forceinline__ float dot_group(const Raw<TPT_TYPE_Q4_0>& r, const Act& a, int) {
+  const uint32_t wa[4] = {r.a.x, r.a.y, r.a.z, r.a.w}, wb[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+  int s0 = 0, s1 = 0, t0 = 0, t1 = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {  // low nibbles: elements 4i.., high nibbles: 16 + 4i..
+    s0 = sdot4((int)(wa[i] & 0x0F0F0F0Fu), a.q[i], s0);
+    s0 = sdot4((int)((wa[i] >> 4) & 0x0F0F0F0Fu), a.q[4 + i], s0);
+    s1 = sdot4((int)(wb[i] & 0x0F0F0F0Fu), a.q[8 + i], s1);
+    s1 = sdot4((int)((wb[i] >> 4) & 0x0F0F0F0Fu), a.q[12 + i], s1);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    t0 = sdot4(0x01010101, a.q[i], t0);
+    t1 = sdot4(0x01010101, a.q[8 + i], t1);
+  }
+  return ((float)(s0 - 8 * t0) * h2f((uint16_t)r.d0)) * a.d0 + ((float)(s1 - 8 * t1) * h2f((uint16_t)r.d1)) * a.d1;
 }
 
 // Q6_K x Q8_K for one group (half p, column half h): vec_dot_q6k_q8k's per-block arithmetic,
@@ -462,7 +537,7 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int 
   constexpr int NPART = RowParts<BPP>::N;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int K = A.K, N = A.N;
-  const bool q80 = WT == TPT_TYPE_Q8_0;
+  const bool q80 = act_q80<WT>();
   const int nb = K / QK_K;  // super-blocks (256 weights) per row
   const Lds L = lds_layout(smem, K, q80);
   const int RPW = geo.rows_per_wg;
@@ -514,7 +589,7 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int 
   // 1. activation values next: the loads complete in issue order, so the prologue below only
   //    waits for these, not for the weights issued after them
   XPre xp;
-  preload_x<WT != TPT_TYPE_Q8_0, NORM>(A, xp);
+  preload_x<!act_q80<WT>(), NORM>(A, xp);
   // every activation load ahead of every weight load, and no prologue arithmetic among them:
   // the prologue then waits only for the former (left alone, the scheduler sinks some
   // activation loads below the weight loads, or hoists the first uses of x above them)
@@ -523,7 +598,7 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int 
   for (int d = 0; d < D; d++) issue(ring[d], d);
   __builtin_amdgcn_sched_barrier(0);
   hook();
-  if constexpr (WT == TPT_TYPE_Q8_0) prologue_q80<NORM ? 1 : 0>(A, xp, L);
+  if constexpr (act_q80<WT>()) prologue_q80<NORM ? 1 : 0>(A, xp, L);
   else prologue_q8k<NORM ? 1 : 0>(A, xp, L);
   barrier_lds();
 

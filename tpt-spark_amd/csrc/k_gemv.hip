@@ -138,6 +138,56 @@ __device__ __forceinline__ void dequant64<TPT_TYPE_Q8_0>(const uint8_t* row, int
   }
 }
 
+template <>
+__device__ __forceinline__ void dequant64<TPT_TYPE_Q5_K>(const uint8_t* row, int g, float* y) {
+  // as Q4_K, values nibble + 16 * bit of qh[l]
+  Raw<TPT_TYPE_Q5_K> r;
+  load_raw<TPT_TYPE_Q5_K>(row, g, r);
+  const int j0 = 2 * (g & 3);
+  auto s = [&](int k) {  // scales byte k: header bytes 4 + k
+    return (int)bsel(k < 4 ? r.h.y : k < 8 ? r.h.z : r.h.w, k & 3);
+  };
+  int sc[2], mn[2];
+#pragma unroll
+  for (int t = 0; t < 2; t++) {
+    const int j = j0 + t;
+    if (j < 4) {
+      sc[t] = s(j) & 63;
+      mn[t] = s(j + 4) & 63;
+    } else {
+      sc[t] = (s(j + 4) & 0xF) | ((s(j - 4) >> 6) << 4);
+      mn[t] = (s(j + 4) >> 4) | ((s(j) >> 6) << 4);
+    }
+  }
+  const float d = h2f((uint16_t)(r.h.x & 0xffff)), dmin = h2f((uint16_t)(r.h.x >> 16));
+  const float d1 = d * (float)sc[0], mm1 = dmin * (float)mn[0];
+  const float d2 = d * (float)sc[1], mm2 = dmin * (float)mn[1];
+  const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+  const uint32_t qh[8] = {r.ha.x, r.ha.y, r.ha.z, r.ha.w, r.hb.x, r.hb.y, r.hb.z, r.hb.w};
+#pragma unroll
+  for (int i = 0; i < 32; i++) {
+    const uint32_t byte = bsel(w[i >> 2], i & 3), hb = bsel(qh[i >> 2], i & 3);
+    y[i] = d1 * (float)((byte & 0xF) + (((hb >> j0) & 1) << 4)) - mm1;
+    y[32 + i] = d2 * (float)((byte >> 4) + (((hb >> (j0 + 1)) & 1) << 4)) - mm2;
+  }
+}
+
+template <>
+__device__ __forceinline__ void dequant64<TPT_TYPE_Q4_0>(const uint8_t* row, int g, float* y) {
+  Raw<TPT_TYPE_Q4_0> r;
+  load_raw<TPT_TYPE_Q4_0>(row, g, r);
+  const float d0 = h2f((uint16_t)r.d0), d1 = h2f((uint16_t)r.d1);
+  const uint32_t wa[4] = {r.a.x, r.a.y, r.a.z, r.a.w}, wb[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const uint32_t ba = bsel(wa[i >> 2], i & 3), bb = bsel(wb[i >> 2], i & 3);
+    y[i] = (float)((int)(ba & 0xF) - 8) * d0;
+    y[16 + i] = (float)((int)(ba >> 4) - 8) * d0;
+    y[32 + i] = (float)((int)(bb & 0xF) - 8) * d1;
+    y[48 + i] = (float)((int)(bb >> 4) - 8) * d1;
+  }
+}
+
 // element offset (within the row) of the e-th value dequant64 produces for group g
 template <int WT>
 __device__ __forceinline__ int elem_of(int g, int e) {
@@ -185,7 +235,7 @@ int launch_cfg(const tpt_ctx* ctx, const GemvArgs& a, int wg_per_cu, hipStream_t
   rpw = (rpw + unit - 1) / unit * unit;
   geo.rows_per_wg = rpw;
   const int grid = (a.N + rpw - 1) / rpw;
-  const size_t lds = lds_act_bytes(a.K, WT == TPT_TYPE_Q8_0) + 4 * (size_t)KS * rpw * NMAT * RowParts<BPP>::N;
+  const size_t lds = lds_act_bytes(a.K, act_q80<WT>()) + 4 * (size_t)KS * rpw * NMAT * RowParts<BPP>::N;
   if (lds > 65536) return fail(TPT_ERR_UNSUPPORTED, "gemv: too many rows per workgroup for LDS");
   const bool norm = a.prologue == PRO_RMSNORM, one = geo.P == KS;  // one pass per k-split wave
   if (norm && one) launch_inst<WT, BPP, RB, NMAT, KS, D, true, true>(a, geo, grid, lds, s, ev0, ev1);
@@ -233,8 +283,10 @@ int launch_gemv_q8(const tpt_ctx* ctx, int wtype, const GemvArgs& a, hipStream_t
     case TPT_TYPE_Q4_K: return two ? dispatch_shape<TPT_TYPE_Q4_K, 2>(ctx, a, s, ev0, ev1) : dispatch_shape<TPT_TYPE_Q4_K, 1>(ctx, a, s, ev0, ev1);
     case TPT_TYPE_Q6_K: return two ? dispatch_shape<TPT_TYPE_Q6_K, 2>(ctx, a, s, ev0, ev1) : dispatch_shape<TPT_TYPE_Q6_K, 1>(ctx, a, s, ev0, ev1);
     case TPT_TYPE_Q8_0: return two ? dispatch_shape<TPT_TYPE_Q8_0, 2>(ctx, a, s, ev0, ev1) : dispatch_shape<TPT_TYPE_Q8_0, 1>(ctx, a, s, ev0, ev1);
+    case TPT_TYPE_Q5_K: return two ? dispatch_shape<TPT_TYPE_Q5_K, 2>(ctx, a, s, ev0, ev1) : dispatch_shape<TPT_TYPE_Q5_K, 1>(ctx, a, s, ev0, ev1);
+    case TPT_TYPE_Q4_0: return two ? dispatch_shape<TPT_TYPE_Q4_0, 2>(ctx, a, s, ev0, ev1) : dispatch_shape<TPT_TYPE_Q4_0, 1>(ctx, a, s, ev0, ev1);
   }
-  return fail(TPT_ERR_UNSUPPORTED, "gemv: weight type must be Q4_K, Q6_K or Q8_0");
+  return fail(TPT_ERR_UNSUPPORTED, "gemv: weight type must be Q4_K, Q5_K, Q6_K, Q8_0 or Q4_0");
 }
 
 int launch_gemv_f32(int wtype, const uint8_t* w, const float* x, float* y, int K, int N,
@@ -246,7 +298,9 @@ int launch_gemv_f32(int wtype, const uint8_t* w, const float* x, float* y, int K
     case TPT_TYPE_Q4_K: hipLaunchKernelGGL(gemv_f32_kernel<TPT_TYPE_Q4_K>, grid, dim3(256), 0, s, w, x, y, K, N, rs); break;
     case TPT_TYPE_Q6_K: hipLaunchKernelGGL(gemv_f32_kernel<TPT_TYPE_Q6_K>, grid, dim3(256), 0, s, w, x, y, K, N, rs); break;
     case TPT_TYPE_Q8_0: hipLaunchKernelGGL(gemv_f32_kernel<TPT_TYPE_Q8_0>, grid, dim3(256), 0, s, w, x, y, K, N, rs); break;
-    default: return fail(TPT_ERR_UNSUPPORTED, "gemv_f32: weight type must be Q4_K, Q6_K or Q8_0");
+    case TPT_TYPE_Q5_K: hipLaunchKernelGGL(gemv_f32_kernel<TPT_TYPE_Q5_K>, grid, dim3(256), 0, s, w, x, y, K, N, rs); break;
+    case TPT_TYPE_Q4_0: hipLaunchKernelGGL(gemv_f32_kernel<TPT_TYPE_Q4_0>, grid, dim3(256), 0, s, w, x, y, K, N, rs); break;
+    default: return fail(TPT_ERR_UNSUPPORTED, "gemv_f32: weight type must be Q4_K, Q5_K, Q6_K, Q8_0 or Q4_0");
   }
   TPT_HIP(hipGetLastError());
   return TPT_OK;

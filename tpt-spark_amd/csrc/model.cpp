@@ -24,7 +24,7 @@ using namespace tpt;
 namespace {
 
 bool matrix_type_ok(int t) {
-  return t == TPT_TYPE_Q4_K || t == TPT_TYPE_Q6_K || t == TPT_TYPE_Q8_0;
+  return t == TPT_TYPE_Q4_K || t == TPT_TYPE_Q5_K || t == TPT_TYPE_Q6_K || t == TPT_TYPE_Q8_0 || t == TPT_TYPE_Q4_0;
 }
 
 const char* type_name(int t) {
@@ -32,6 +32,8 @@ const char* type_name(int t) {
     case TPT_TYPE_F32: return "F32";
     case TPT_TYPE_F16: return "F16";
     case TPT_TYPE_Q8_0: return "Q8_0";
+    case TPT_TYPE_Q4_0: return "Q4_0";
+    case TPT_TYPE_Q5_K: return "Q5_K";
     case TPT_TYPE_Q4_K: return "Q4_K";
     case TPT_TYPE_Q6_K: return "Q6_K";
   }

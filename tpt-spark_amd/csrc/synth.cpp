@@ -23,11 +23,11 @@
 
 namespace {
 
-enum { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
+enum { T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14 };
 
-int blk_elems(int t) { return t == T_Q4_K || t == T_Q6_K ? 256 : t == T_Q8_0 ? 32 : 1; }
+int blk_elems(int t) { return t == T_Q4_K || t == T_Q5_K || t == T_Q6_K ? 256 : t == T_Q8_0 || t == T_Q4_0 ? 32 : 1; }
 int blk_bytes(int t) {
-  return t == T_Q4_K ? 144 : t == T_Q6_K ? 210 : t == T_Q8_0 ? 34 : t == T_F16 ? 2 : 4;
+  return t == T_Q4_K ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 210 : t == T_Q8_0 ? 34 : t == T_Q4_0 ? 18 : t == T_F16 ? 2 : 4;
 }
 
 uint16_t f32_to_f16(float v) {  // round to nearest even
@@ -141,6 +141,78 @@ void quant_q4k(const float* x, uint8_t* out) {
     for (int l = 0; l < 32; l++) qs[32 * g + l] = (uint8_t)(q[64 * g + l] | (q[64 * g + 32 + l] << 4));
 }
 
+// ---- Q5_K: Q4_K's scales with 5-bit values (31 levels); the fifth bits go to qh (bit 2g of
+// qh[l] for element 64g + l, bit 2g + 1 for element 64g + 32 + l)
+void quant_q5k(const float* x, uint8_t* out) {
+  float scale[8], mn[8];
+  for (int j = 0; j < 8; j++) {
+    float lo = x[32 * j], hi = x[32 * j];
+    for (int l = 1; l < 32; l++) {
+      lo = std::min(lo, x[32 * j + l]);
+      hi = std::max(hi, x[32 * j + l]);
+    }
+    lo = std::min(lo, 0.f);
+    scale[j] = (hi - lo) / 31.f;
+    mn[j] = -lo;
+  }
+  float ms = 0, mm = 0;
+  for (int j = 0; j < 8; j++) {
+    ms = std::max(ms, scale[j]);
+    mm = std::max(mm, mn[j]);
+  }
+  const uint16_t dh = f32_to_f16(ms / 63.f), mh = f32_to_f16(mm / 63.f);
+  const float d = f16_to_f32(dh), dmin = f16_to_f32(mh);
+  int sc[8], m[8];
+  for (int j = 0; j < 8; j++) {
+    sc[j] = d > 0 ? std::min(63, std::max(0, nearest(scale[j] / d))) : 0;
+    m[j] = dmin > 0 ? std::min(63, std::max(0, nearest(mn[j] / dmin))) : 0;
+  }
+  uint8_t* s = out + 4;
+  memcpy(out, &dh, 2);
+  memcpy(out + 2, &mh, 2);
+  for (int j = 0; j < 4; j++) {
+    s[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+    s[j + 4] = (uint8_t)((m[j] & 63) | ((m[j + 4] >> 4) << 6));
+    s[j + 8] = (uint8_t)((sc[j + 4] & 0xF) | ((m[j + 4] & 0xF) << 4));
+  }
+  uint8_t q[256];
+  for (int j = 0; j < 8; j++) {
+    const float ds = d * (float)sc[j], dm = dmin * (float)m[j];
+    for (int l = 0; l < 32; l++) {
+      const int v = ds > 0 ? nearest((x[32 * j + l] + dm) / ds) : 0;
+      q[32 * j + l] = (uint8_t)std::min(31, std::max(0, v));
+    }
+  }
+  uint8_t* qh = out + 16;
+  uint8_t* qs = out + 48;
+  memset(qh, 0, 32);
+  for (int g = 0; g < 4; g++)
+    for (int l = 0; l < 32; l++) {
+      const int lo = q[64 * g + l], hi = q[64 * g + 32 + l];
+      qs[32 * g + l] = (uint8_t)((lo & 15) | ((hi & 15) << 4));
+      qh[l] |= (uint8_t)(((lo >> 4) << (2 * g)) | ((hi >> 4) << (2 * g + 1)));
+    }
+}
+
+// ---- Q4_0: per 32, d = (signed value of the largest magnitude) / -8, q = x / d + 8 in [0, 15];
+// element j < 16 in the low nibble of qs[j], element j + 16 in its high nibble
+void quant_q4_0(const float* x, uint8_t* out) {
+  float amax = 0, mx = 0;
+  for (int l = 0; l < 32; l++)
+    if (fabsf(x[l]) > amax) {
+      amax = fabsf(x[l]);
+      mx = x[l];
+    }
+  const uint16_t dh = f32_to_f16(mx / -8.f);
+  const float d = f16_to_f32(dh), id = d != 0.f ? 1.f / d : 0.f;
+  memcpy(out, &dh, 2);
+  for (int j = 0; j < 16; j++) {
+    const int a = std::min(15, std::max(0, (int)(x[j] * id + 8.5f)));
+    const int b = std::min(15, std::max(0, (int)(x[j + 16] * id + 8.5f)));
+    out[2 + j] = (uint8_t)(a | (b << 4));
+  }
+}
+
 // ---- Q6_K: 16 sub-blocks of 16, int8 scales under an f16 d, 6-bit q - 32
 void quant_q6k(const float* x, uint8_t* out) {
   float s[16];
@@ -193,6 +265,8 @@ int quantize(int type, const float* x, int64_t n, uint8_t* out) {
     uint8_t* o = out + b * bb;
     switch (type) {
       case T_Q4_K: quant_q4k(xs, o); break;
+      case T_Q5_K: quant_q5k(xs, o); break;
+      case T_Q4_0: quant_q4_0(xs, o); break;
       case T_Q6_K: quant_q6k(xs, o); break;
       case T_Q8_0: quant_q8_0(xs, o); break;
       case T_F32: memcpy(o, xs, 4); break;

@@ -27,10 +27,12 @@ static_assert(sizeof(BlockQ6K) == 210, "q6k");
 static_assert(sizeof(BlockQ8_0) == 34, "q8_0");
 
 __host__ __device__ inline int type_block(int t) {
-  return t == TPT_TYPE_Q4_K || t == TPT_TYPE_Q6_K ? QK_K : t == TPT_TYPE_Q8_0 ? QK8_0 : 1;
+  return t == TPT_TYPE_Q4_K || t == TPT_TYPE_Q5_K || t == TPT_TYPE_Q6_K ? QK_K
+         : t == TPT_TYPE_Q8_0 || t == TPT_TYPE_Q4_0 ? QK8_0 : 1;
 }
 __host__ __device__ inline int type_bytes(int t) {
-  return t == TPT_TYPE_Q4_K ? 144 : t == TPT_TYPE_Q6_K ? 210 : t == TPT_TYPE_Q8_0 ? 34
+  return t == TPT_TYPE_Q4_K ? 144 : t == TPT_TYPE_Q5_K ? 176 : t == TPT_TYPE_Q6_K ? 210
+         : t == TPT_TYPE_Q8_0 ? 34 : t == TPT_TYPE_Q4_0 ? 18
          : t == TPT_TYPE_F16 ? 2 : t == TPT_TYPE_F32 ? 4 : 0;
 }
 inline size_t row_bytes(int t, int64_t k) { return (size_t)(k / type_block(t)) * type_bytes(t); }
@@ -202,6 +204,30 @@ __device__ __forceinline__ float dequant_elem(int type, const uint8_t* base, int
   if (type == TPT_TYPE_Q8_0) {
     const uint8_t* b = base + (i >> 5) * 34;
     return h2f(ldg_u<uint16_t>(b)) * (float)(int8_t)b[2 + (i & 31)];
+  }
+  if (type == TPT_TYPE_Q5_K) {  // Q4_K's layout plus bit (2 group + half) of qh[l]
+    const uint8_t* b = base + (i >> 8) * 176;
+    const int j = (int)(i & 255), g = j >> 6, half = (j >> 5) & 1, l = j & 31, sub = 2 * g + half;
+    const uint8_t qb = b[48 + 32 * g + l];
+    const int q = (half ? (qb >> 4) : (qb & 0xF)) + (((b[16 + l] >> sub) & 1) << 4);
+    const uint8_t* s = b + 4;
+    int sc, m;
+    if (sub < 4) {
+      sc = s[sub] & 63;
+      m = s[sub + 4] & 63;
+    } else {
+      sc = (s[sub + 4] & 0xF) | ((s[sub - 4] >> 6) << 4);
+      m = (s[sub + 4] >> 4) | ((s[sub] >> 6) << 4);
+    }
+    const float d = h2f(ldg_u<uint16_t>(b)), dmin = h2f(ldg_u<uint16_t>(b + 2));
+    const float d1 = d * (float)sc, m1 = dmin * (float)m;
+    return d1 * (float)q - m1;
+  }
+  if (type == TPT_TYPE_Q4_0) {  // element j < 16: low nibble of qs[j]; j + 16: its high nibble
+    const uint8_t* b = base + (i >> 5) * 18;
+    const int j = (int)(i & 31);
+    const int q = j < 16 ? (b[2 + j] & 0xF) : (b[2 + j - 16] >> 4);
+    return (float)(q - 8) * h2f(ldg_u<uint16_t>(b));
   }
   if (type == TPT_TYPE_F16) return h2f(ldg_u<uint16_t>(base + 2 * i));
   return ldg_u<float>(base + 4 * i);

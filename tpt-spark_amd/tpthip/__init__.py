@@ -16,9 +16,11 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 
-TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K = 0, 1, 8, 12, 14
-BLOCK = {TYPE_F32: 1, TYPE_F16: 1, TYPE_Q8_0: 32, TYPE_Q4_K: 256, TYPE_Q6_K: 256}
-TYPE_SIZE = {TYPE_F32: 4, TYPE_F16: 2, TYPE_Q8_0: 34, TYPE_Q4_K: 144, TYPE_Q6_K: 210}
+TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K = 0, 1, 2, 8, 12, 13, 14
+BLOCK = {TYPE_F32: 1, TYPE_F16: 1, TYPE_Q4_0: 32, TYPE_Q8_0: 32, TYPE_Q4_K: 256, TYPE_Q5_K: 256,
+         TYPE_Q6_K: 256}
+TYPE_SIZE = {TYPE_F32: 4, TYPE_F16: 2, TYPE_Q4_0: 18, TYPE_Q8_0: 34, TYPE_Q4_K: 144, TYPE_Q5_K: 176,
+             TYPE_Q6_K: 210}
 ACT_Q8, ACT_F32, ACT_F16 = 0, 1, 2
 
 ERR_INVALID, ERR_HIP, ERR_IO, ERR_FORMAT, ERR_UNSUPPORTED, ERR_CANCELLED, ERR_STATE, ERR_OOM = \
