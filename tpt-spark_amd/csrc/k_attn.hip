@@ -222,15 +222,30 @@ __global__ void __launch_bounds__(ANT) attn_merge_kernel(const float* __restrict
   const int L = (state ? state->pos + 1 : L_host) + t;
   nch = min(nch, (L + CL - 1) / CL);
   if (tid < WAVE) {
+    // each chunk's max and sum in one round trip (at most NCH_MAX / WAVE chunks per lane)
+    constexpr int CPL = NCH_MAX / WAVE;
+    float mv[CPL], lv[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; i++) {
+      const int c = lane + i * WAVE;
+      const float* rec = pk + (size_t)min(c, nch - 1) * G * PSTRIDE;
+      mv[i] = rec[HD];
+      lv[i] = rec[HD + 1];
+    }
     float mm = -INFINITY;
-    for (int c = lane; c < nch; c += WAVE) mm = fmaxf(mm, pk[(size_t)c * G * PSTRIDE + HD]);
+#pragma unroll
+    for (int i = 0; i < CPL; i++)
+      if (lane + i * WAVE < nch) mm = fmaxf(mm, mv[i]);
     mm = wave_max_dpp(mm);
     float ls = 0.f;
-    for (int c = lane; c < nch; c += WAVE) {
-      const float* rec = pk + (size_t)c * G * PSTRIDE;
-      const float w = expf(rec[HD] - mm);
-      s_w[c] = w;
-      ls = fmaf(w, rec[HD + 1], ls);
+#pragma unroll
+    for (int i = 0; i < CPL; i++) {
+      const int c = lane + i * WAVE;
+      if (c < nch) {
+        const float w = expf(mv[i] - mm);
+        s_w[c] = w;
+        ls = fmaf(w, lv[i], ls);
+      }
     }
     ls = wave_sum_dpp(ls);
     if (lane == 0) s_l = ls;
