@@ -359,8 +359,15 @@ int gemm_prepare(tpt_ctx* c, int type, const void* w, const float* x, float* y, 
   // fp16 rows [M][K], then (GEMM_Q8K) block scales [M][K/256] and per-16 sums [M][K/16]
   const size_t o_d = (mk * 2 + 255) & ~(size_t)255;
   const size_t o_s = o_d + (((size_t)M * (K / 256) * 4 + 255) & ~(size_t)255);
-  const size_t bytes = g.mode == GEMM_Q8K ? o_s + (size_t)M * (K / 16) * 2 : mk * 2;
+  const size_t act_bytes = g.mode == GEMM_Q8K ? o_s + (size_t)M * (K / 16) * 2 : mk * 2;
+  // split-K workspace when the output tiles cannot fill the device
+  const int ns = gemm_splits(M, N, K);
+  const size_t o_p = (act_bytes + 255) & ~(size_t)255;
+  const size_t pf = ns > 1 ? (size_t)ns * M * N : 0;
+  const size_t bytes = o_p + pf * 4;
   TPT_HIP(hipMallocAsync(&call->scratch, bytes, c->stream));
+  g.part = pf ? (float*)((uint8_t*)call->scratch + o_p) : nullptr;
+  g.part_floats = pf;
   uint8_t* base = (uint8_t*)call->scratch;
   p.af = (uint16_t*)base;
   g.af = p.af;

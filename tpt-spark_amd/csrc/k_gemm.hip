@@ -30,6 +30,8 @@
 // no workgroup converts it again.
 #include <hip/hip_ext.h>
 
+#include <algorithm>
+
 #include "kernels.h"
 
 namespace tpt {
@@ -361,7 +363,9 @@ __global__ void __launch_bounds__(GT, 1) gemm_kernel(const GemmArgs g) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int wm = wid >> 2, wn = wid & 3;  // wave tile: rows 64 wm .., cols 32 wn ..
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  const int nkb = g.K / 256;
+  // split-K (small M): split blockIdx.z of gridDim.z takes super-blocks [kb0, kb1)
+  const int nkb_all = g.K / 256, ns = gridDim.z, sz = blockIdx.z;
+  const int kb0 = sz * nkb_all / ns, nkb = (sz + 1) * nkb_all / ns;
   const int lr = lane & 31;
   // chains: Q4_K q8k acc0 / acc1 = the two halves of a super-block; Q6_K q8k acc0 / acc1 =
   // hi / lo over the whole super-block; fp16 mode: out directly
@@ -377,11 +381,11 @@ __global__ void __launch_bounds__(GT, 1) gemm_kernel(const GemmArgs g) {
 
   // prologue: step 0 in LDS, step 1 in registers
   Stage<WT> st;
-  stage_load<WT, MODE, 0>(g, m0, n0, 0, st);
-  stage_store<WT, MODE, 0>(st, s.t[0], s.blk[0]);
-  stage_load<WT, MODE, 1>(g, m0, n0, 0, st);
+  stage_load<WT, MODE, 0>(g, m0, n0, kb0, st);
+  stage_store<WT, MODE, 0>(st, s.t[0], s.blk[kb0 & 1]);
+  stage_load<WT, MODE, 1>(g, m0, n0, kb0, st);
   __syncthreads();
-  for (int kb = 0; kb < nkb; kb++) {
+  for (int kb = kb0; kb < nkb; kb++) {
     // past the last block the next block is the last one again (clamped), staged into the tile
     // and block buffer that are not read again
     const int kn = kb + 1 < nkb ? kb + 1 : kb;
@@ -405,7 +409,7 @@ __global__ void __launch_bounds__(GT, 1) gemm_kernel(const GemmArgs g) {
     __syncthreads();
   }
 
-  // epilogue: y[m][n] = out (+ resid[m][n])
+  // epilogue: y[m][n] = out (+ resid[m][n]); split-K: this split's partial sums
   const int n = n0 + 32 * wn + lr;
 #pragma unroll
   for (int i = 0; i < 2; i++)
@@ -414,10 +418,25 @@ __global__ void __launch_bounds__(GT, 1) gemm_kernel(const GemmArgs g) {
       const int m = m0 + 64 * wm + 32 * i + (e / 4) * 8 + (lane >> 5) * 4 + (e % 4);
       if (m < g.M && n < g.N) {
         float v = out[i][e];
-        if (g.resid) v = v + g.resid[(size_t)m * g.ldr + n];
-        g.y[(size_t)m * g.ldy + n] = v;
+        if (ns > 1) {
+          g.part[((size_t)sz * g.M + m) * g.N + n] = v;
+        } else {
+          if (g.resid) v = v + g.resid[(size_t)m * g.ldr + n];
+          g.y[(size_t)m * g.ldy + n] = v;
+        }
       }
     }
+}
+
+// Split-K sum: y[m][n] = sum over splits s = 0, 1, .. of part[s][m][n] (+ resid[m][n])
+__global__ void __launch_bounds__(256) gemm_split_reduce_kernel(const GemmArgs g, int ns) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, mn = (size_t)g.M * g.N;
+  if (i >= mn) return;
+  const int m = (int)(i / g.N), n = (int)(i % g.N);
+  float v = g.part[i];
+  for (int k = 1; k < ns; k++) v = v + g.part[(size_t)k * mn + i];
+  if (g.resid) v = v + g.resid[(size_t)m * g.ldr + n];
+  g.y[(size_t)m * g.ldy + n] = v;
 }
 
 // One workgroup (4 waves) per activation row: optional SwiGLU (candle: silu(w1 x) * (w3 x)),
@@ -512,16 +531,36 @@ int launch_gemm_timed(const GemmArgs& g, hipStream_t s, hipEvent_t ev0, hipEvent
     return fail(TPT_ERR_INVALID, "gemm: Q4_K weight rows must be 16-byte aligned");
   if (g.wtype == TPT_TYPE_Q6_K && ((g.w_stride % 2) || ((uintptr_t)g.w % 2)))
     return fail(TPT_ERR_INVALID, "gemm: Q6_K weight rows must be 2-byte aligned");
-  const dim3 grid((unsigned)((g.N + BN - 1) / BN), (unsigned)((g.M + BM - 1) / BM));
+  int ns = gemm_splits(g.M, g.N, g.K);
+  if (!g.part || g.part_floats < (size_t)ns * g.M * g.N) ns = 1;  // no workspace: one pass over K
+  const dim3 grid((unsigned)((g.N + BN - 1) / BN), (unsigned)((g.M + BM - 1) / BM), (unsigned)ns);
+  hipEvent_t e1 = ns > 1 ? nullptr : ev1;  // split-K: the stop event goes on the sum kernel
   if (g.wtype == TPT_TYPE_Q4_K) {
-    if (g.mode == GEMM_Q8K) hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q4_K, GEMM_Q8K>), grid, dim3(GT), 0, s, ev0, ev1, 0, g);
-    else hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q4_K, GEMM_F16>), grid, dim3(GT), 0, s, ev0, ev1, 0, g);
+    if (g.mode == GEMM_Q8K) hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q4_K, GEMM_Q8K>), grid, dim3(GT), 0, s, ev0, e1, 0, g);
+    else hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q4_K, GEMM_F16>), grid, dim3(GT), 0, s, ev0, e1, 0, g);
   } else {
-    if (g.mode == GEMM_Q8K) hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q6_K, GEMM_Q8K>), grid, dim3(GT), 0, s, ev0, ev1, 0, g);
-    else hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q6_K, GEMM_F16>), grid, dim3(GT), 0, s, ev0, ev1, 0, g);
+    if (g.mode == GEMM_Q8K) hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q6_K, GEMM_Q8K>), grid, dim3(GT), 0, s, ev0, e1, 0, g);
+    else hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q6_K, GEMM_F16>), grid, dim3(GT), 0, s, ev0, e1, 0, g);
   }
   TPT_HIP(hipGetLastError());
+  if (ns > 1) {
+    const size_t mn = (size_t)g.M * g.N;
+    hipExtLaunchKernelGGL(gemm_split_reduce_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s,
+                          nullptr, ev1, 0, g, ns);
+    TPT_HIP(hipGetLastError());
+  }
   return TPT_OK;
+}
+
+// Splits of K for an M x N x K GEMM whose output has fewer tiles than the 256 CUs: the most
+// that still run in one round (tiles x splits <= 256), at least two super-blocks per split, at
+// most 8.
+int gemm_splits(int M, int N, int K) {
+  const int tiles = ((N + BN - 1) / BN) * ((M + BM - 1) / BM), nkb = K / 256;
+  if (tiles > 128 || nkb < 4) return 1;
+  int ns = 256 / tiles;
+  ns = std::min(ns, nkb / 2);
+  return std::min(ns, 8);
 }
 
 }  // namespace tpt

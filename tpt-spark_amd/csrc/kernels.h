@@ -71,7 +71,12 @@ struct GemmArgs {
   int ldy = 0;
   const float* resid = nullptr;      // optional: y = X.W^T + resid
   int ldr = 0;
+  // optional split-K workspace (f32): with at least gemm_splits(M, N, K) * M * N floats a
+  // launch whose output tiles cannot fill the device splits K and sums the splits in order
+  float* part = nullptr;
+  size_t part_floats = 0;
 };
+int gemm_splits(int M, int N, int K);
 int launch_gemm(const GemmArgs& g, hipStream_t s);
 // the same launch with dispatch-stamped start/stop events (hipExtLaunchKernelGGL)
 int launch_gemm_timed(const GemmArgs& g, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1);

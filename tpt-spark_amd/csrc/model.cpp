@@ -623,6 +623,14 @@ int tpt_model::prefill_scratch(int T, int n_chunks) {
                o_att = carve((size_t)T * qd * 4), o_g = carve((size_t)T * F * 4), o_u = carve((size_t)T * F * 4),
                o_part = carve((size_t)T * attn_part_floats(desc.n_heads, desc.n_kv_heads, desc.head_dim, n_chunks) * 4),
                o_ids = carve((size_t)T * 4);
+  // split-K workspace of the GEMMs (short prompts): the largest splits x T x N over the shapes
+  size_t gsplit = 0;
+  for (const int* kn : {(const int[2]){H, qd + 2 * kd}, (const int[2]){qd, H}, (const int[2]){H, F},
+                        (const int[2]){F, H}}) {
+    const int ns = gemm_splits(T, kn[1], kn[0]);
+    if (ns > 1) gsplit = std::max(gsplit, (size_t)ns * T * kn[1]);
+  }
+  const size_t o_gsplit = carve(gsplit * 4);
   if (off > pf_bytes) {
     if (pf_mem) {
       TPT_HIP(hipStreamSynchronize(stream));
@@ -645,6 +653,8 @@ int tpt_model::prefill_scratch(int T, int n_chunks) {
   pf_u = (float*)(b + o_u);
   pf_part = (float*)(b + o_part);
   pf_ids = (uint32_t*)(b + o_ids);
+  pf_gsplit = gsplit ? (float*)(b + o_gsplit) : nullptr;
+  pf_gsplit_floats = gsplit;
   return TPT_OK;
 }
 
@@ -690,6 +700,7 @@ int tpt_model::batched_layers(int T, int p0, int l0, int l1) {
     g.w = w; g.w_stride = row_bytes(type, K);
     g.af = pf_af; g.ad = pf_ad; g.as16 = pf_as16;
     g.y = y; g.ldy = ldy; g.resid = resid; g.ldr = ldy;
+    g.part = pf_gsplit; g.part_floats = pf_gsplit_floats;
     return launch_gemm(g, stream);
   };
   for (int l = l0; l < l1; l++) {

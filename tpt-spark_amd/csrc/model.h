@@ -65,6 +65,8 @@ struct tpt_model {
   static constexpr int kPrefillT = 2048;
   bool batched_prefill = false;       // every layer matrix is Q4_K
   bool causal_mfma = true;            // prompt attention on the matrix cores where supported
+  float* pf_gsplit = nullptr;         // split-K workspace of the prefill GEMMs (short prompts)
+  size_t pf_gsplit_floats = 0;
   void* pf_mem = nullptr;             // scratch of the batched prefill, grown on demand
   size_t pf_bytes = 0;
   float *pf_x = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_att = nullptr, *pf_g = nullptr,
