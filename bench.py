@@ -22,9 +22,13 @@ shapes (`attn_decode_f16`, GB/s vs HBM peak over rotating caches), the MFMA pref
 prompt shapes (`prefill_gemm_q4k`, TFLOP/s vs the 2.5 PFLOP/s dense fp16 peak) and the
 matrix-core causal prompt attention (`prefill_attn_causal_f16`, algorithmic TFLOP/s, same peak).
 
+Also in `config`: the Q6_K and Q8_0 GEMVs at the same four shapes (`gemv_q6k`, `gemv_q8_0`).
+
 cpu_baseline: the CPU oracle's restatement of candle's CPU decode (Q8_K activation quant,
 integer vec_dot, OpenMP over output columns) timed on this host's cores on a bounded sample of
-the same model: a short prompt, then greedy decode steps for about 20 s.
+the same model at the GPU run's decode positions (its KV cache primed with as many positions as
+the prompt), greedy decode steps for about 20 s; nproc, the CPU model and the thread count are
+recorded.
 """
 import argparse
 import json
@@ -64,23 +68,31 @@ def copy_calibration(ctx, iters=4):
     return {"bytes_read": COPY_BYTES, "bytes_written": COPY_BYTES, "us_per_launch": round(ms / iters * 1e3, 2)}
 
 
-def gemv_roofline(tp, ctx, iters=256):
-    """Event-timed Q4_K GEMV at the config-2 shapes, rotating through >= 1 GB of copies."""
+GEMV_SHAPES = [(4096, 14336), (14336, 4096), (4096, 4096), (4096, 1024)]
+
+
+def gemv_roofline(tp, ctx, iters=256, qtype=None):
+    """Event-timed fused dequant-GEMV at the config-2 shapes (K -> N), rotating through >= 1 GB
+    of weight copies.  Algorithmic bytes per launch = the quantized weight blocks (Q4_K 144 B,
+    Q6_K 210 B per 256 weights, Q8_0 34 B per 32) + fp32 x + fp32 y."""
     from tpthip import synth
+    qtype = tp.TYPE_Q4_K if qtype is None else qtype
+    name = {tp.TYPE_Q4_K: "q4_k", tp.TYPE_Q6_K: "q6_k", tp.TYPE_Q8_0: "q8_0"}[qtype]
     out = {}
-    for K, N in [(4096, 14336), (14336, 4096), (4096, 4096), (4096, 1024)]:
-        w = synth.random_weights(tp.TYPE_Q4_K, N, K, seed=K + N, name=f"bench{K}x{N}")
+    for K, N in GEMV_SHAPES:
+        w = synth.random_weights(qtype, N, K, seed=K + N, name=f"bench{K}x{N}")
         n_copies = max(2, int(np.ceil(1.1e9 / w.nbytes)))
         bufs = [ctx.to_device(w) for _ in range(n_copies)]
         x = ctx.to_device(np.random.default_rng(1).standard_normal(K).astype(np.float32))
         y = ctx.alloc(N * 4)
-        ctx.bench_gemv(tp.TYPE_Q4_K, bufs, x, y, K, N, n_copies)  # warm-up pass
-        ms = ctx.bench_gemv(tp.TYPE_Q4_K, bufs, x, y, K, N, iters)
-        alg = K * N * 144 // 256 + 4 * K + 4 * N
+        ctx.bench_gemv(qtype, bufs, x, y, K, N, n_copies)  # warm-up pass
+        ms = ctx.bench_gemv(qtype, bufs, x, y, K, N, iters)
+        alg = K * N // tp.BLOCK[qtype] * tp.TYPE_SIZE[qtype] + 4 * K + 4 * N
         us = ms * 1e3 / iters
-        out[f"{K}x{N}"] = {"bytes": alg, "us_per_launch": round(us, 3),
-                           "gbs": round(alg / (us * 1e-6) / 1e9, 1), "copies": n_copies}
-        log(f"gemv q4_k {K}->{N}: {us:.2f} us/launch, {alg / (us * 1e-6) / 1e9:.0f} GB/s")
+        gbs = alg / (us * 1e-6) / 1e9
+        out[f"{K}x{N}"] = {"bytes": alg, "us_per_launch": round(us, 3), "gbs": round(gbs, 1),
+                           "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": n_copies}
+        log(f"gemv {name} {K}->{N}: {us:.2f} us/launch, {gbs:.0f} GB/s")
         for b in bufs:
             b.free()
     return out
@@ -88,7 +100,7 @@ def gemv_roofline(tp, ctx, iters=256):
 
 # decode attention at the long-context shapes: GQA 32/8 hd 128 and MHA 32/32 hd 96, fp16 cache
 ATTN_CASES = [(32, 8, 128, 512), (32, 8, 128, 4096), (32, 8, 128, 16384), (32, 8, 128, 32768),
-              (32, 32, 96, 4096), (32, 32, 96, 16384)]
+              (32, 32, 96, 512), (32, 32, 96, 4096), (32, 32, 96, 16384), (32, 32, 96, 32768)]
 
 
 def attn_roofline(tp, ctx, iters=64):
@@ -179,26 +191,56 @@ def gemm_roofline(tp, ctx, iters=20):
     return out
 
 
-def cpu_baseline(path, budget_s=20.0):
+def host_cpu():
+    """nproc, the threads this process may run on, and the CPU model (lscpu's "Model name")."""
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except AttributeError:
+        allowed = os.cpu_count() or 1
+    return os.cpu_count() or 1, allowed, model
+
+
+def cpu_baseline(path, pos0, budget_s=20.0):
+    """The oracle (candle's CPU decode restated: Q8_K activations, integer vec_dot, OpenMP over
+    output columns) decoding the same model at the GPU run's positions: its f32 KV cache primed
+    with pos0 synthetic positions (a real 2048-token CPU prefill would take minutes; the decode
+    step's work depends on how many positions it reads, not on their values), then greedy steps
+    for about budget_s seconds.  Threads: the CPU share this process is given (the affinity
+    mask, capped by OMP_NUM_THREADS when set); nproc and the CPU model are recorded."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
-    threads = min(os.cpu_count() or 1, 16)
+    nproc, allowed, model = host_cpu()
+    threads = allowed
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
     m = oracle.Model(path)
-    m.reset(64)
+    m.reset(pos0 + 512)
+    m.prime_cache(pos0, SEED)
     rng = np.random.default_rng(SEED)
-    prompt = rng.integers(0, m.cfg["vocab"], 4).tolist()
-    logits = m.forward(prompt, 0, threads)
-    tok = oracle.argmax(logits)
-    pos, n, t0 = len(prompt), 0, time.perf_counter()
-    while time.perf_counter() - t0 < budget_s and pos < 64:
+    tok = int(rng.integers(0, m.cfg["vocab"]))
+    pos, n = pos0, 0
+    tok = oracle.argmax(m.forward([tok], pos, threads))  # first step untimed (page-in)
+    pos += 1
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s and pos < pos0 + 512:
         tok = oracle.argmax(m.forward([tok], pos, threads))
         pos += 1
         n += 1
     dt = time.perf_counter() - t0
     m.close()
     return {"value": round(n / dt, 4), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"8B-shape Q4_K_M, 4-token prompt then {n} greedy decode steps "
-                      f"({dt:.1f} s) on {threads} host threads"}
+            "nproc": nproc, "cpu_model": model, "positions": [pos0 + 1, pos - 1],
+            "sample": f"8B-shape Q4_K_M (the benchmark's model), f32 KV cache primed with {pos0} "
+                      f"synthetic positions, then {n} timed greedy decode steps at positions "
+                      f"{pos0 + 1}-{pos - 1} ({dt:.1f} s) on {threads} threads (nproc {nproc})"}
 
 
 def traffic_from_profiles(shape):
@@ -257,6 +299,8 @@ def main():
     if args.leg == "gemv":
         print(json.dumps({"gemv": gemv, "copy": copy_calibration(ctx)}))
         return
+    gemv_q6k = gemv_roofline(tp, ctx, iters=64, qtype=tp.TYPE_Q6_K)
+    gemv_q80 = gemv_roofline(tp, ctx, iters=64, qtype=tp.TYPE_Q8_0)
     attn = attn_roofline(tp, ctx)
     gemm = gemm_roofline(tp, ctx)
     causal = attn_causal_roofline(tp, ctx)
@@ -301,7 +345,7 @@ def main():
         log(f"prefill {len(prompt)} tok in {st.ttft_ms:.0f} ms ({prefill_tok_s:.1f} tok/s); decode "
             f"{args.steps} tok in {st.decode_ms:.1f} ms = {tok_s:.1f} tok/s; ceiling {ceiling:.1f}")
         eng.close()
-        cpu = None if args.no_cpu else cpu_baseline(path)
+        cpu = None if args.no_cpu else cpu_baseline(path, len(prompt))
     finally:
         if not args.model and os.path.exists(path):
             os.remove(path)
@@ -336,6 +380,8 @@ def main():
             "decode_frac_of_ceiling_with_kv": round(tok_s / (HBM_PEAK_GBS * 1e9 / (bpt + kv_bpt)), 4),
             "arith": "q4_k/q6_k weights x q8_k activations: int8 dot4 -> int32, f32 block scales",
             "gemv_q4k": gemv,
+            "gemv_q6k": gemv_q6k,
+            "gemv_q8_0": gemv_q80,
             "attn_decode_f16": attn,
             "prefill_gemm_q4k": gemm,
             "prefill_attn_causal_f16": causal,

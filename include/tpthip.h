@@ -189,6 +189,12 @@ typedef void (*tpt_progress_fn)(void* user, uint32_t done, uint32_t total);
  * keeps: the CandleEngine-exact mode). */
 int tpt_model_load(tpt_ctx* ctx, const char* gguf_path, int max_ctx, int kv_type,
                    tpt_progress_fn progress, void* user, tpt_model** out);
+/* Host only (no device, no context): parse and validate a GGUF as tpt_model_load would --
+ * metadata keys and defaults, architecture, every tensor the forward pass reads present with the
+ * shape, type and byte size the kernels assume, no tensor past the end of the file -- and fill
+ * *out (max_ctx and kv_type left 0).  Replaces extract_meta (wgpu_loader.rs:305-406) and the
+ * validation half of load_gguf_to_vram (wgpu_loader.rs:105-135). */
+int tpt_model_inspect(const char* gguf_path, tpt_model_desc* out);
 int tpt_model_describe(const tpt_model* m, tpt_model_desc* out);
 int tpt_model_destroy(tpt_model* m);
 

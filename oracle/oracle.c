@@ -587,7 +587,13 @@ void orc_rope_i(float* x, int n_heads, int hd, const float* c, const float* s) {
 }
 
 /* quantized_llama LayerWeights::forward_attn, non-metal branch: repeat_kv (head h reads kv
- * head h / (nq/nkv)), scores = (q.k) * f32(1/sqrt(hd)), softmax_last_dim, p.v */
+ * head h / (nq/nkv)), scores = (q.k) * f32(1/sqrt(hd)), softmax_last_dim, p.v.  The two products
+ * are candle's f32 matmul, i.e. the gemm crate (gemm 0.17.1, Cargo.lock), which picks its kernel
+ * at run time by CPU feature: on a host with FMA (every x86-64-v3 part, which this library is
+ * built for) each output accumulates fused multiply-adds in order along the reduced dimension,
+ * on a host without FMA separate multiplies and adds.  fma = 1 restates the first (the default
+ * of the model and of orc_attention), fma = 0 the second (a test instrument: the spread between
+ * them is how far candle's own result moves between hosts). */
 static void attention_impl(const float* q, const float* kc, const float* vc, int nq, int nkv, int hd,
                            int L, int L_stride, float* o, int fma) {
   const float scale = (float)(1.0 / sqrt((double)hd));
@@ -624,7 +630,7 @@ static void attention_impl(const float* q, const float* kc, const float* vc, int
 
 void orc_attention(const float* q, const float* kc, const float* vc, int nq, int nkv, int hd,
                    int L, int L_stride, float* o) {
-  attention_impl(q, kc, vc, nq, nkv, hd, L, L_stride, o, 0);
+  attention_impl(q, kc, vc, nq, nkv, hd, L, L_stride, o, 1);
 }
 
 /* f32::total_cmp key */
@@ -785,6 +791,7 @@ static int kv_f32(const orc_model* m, const char* key, float* out) {
 orc_model* orc_model_open(const char* path, char* err, int errlen) {
 #define FAIL(...) do { if (err) snprintf(err, (size_t)errlen, __VA_ARGS__); orc_model_close(m); return NULL; } while (0)
   orc_model* m = (orc_model*)calloc(1, sizeof(orc_model));
+  if (m) m->attn_fma = 1; /* candle's gemm crate on an FMA host (the x86-64-v3 hosts this runs on) */
   int fd = open(path, O_RDONLY);
   if (fd < 0) FAIL("open %s failed", path);
   struct stat st;
@@ -1029,6 +1036,35 @@ int orc_model_kv(const orc_model* m, int layer, float* k_out, float* v_out) {
   const size_t n = (size_t)c->n_kv_heads * m->max_pos * c->head_dim;
   memcpy(k_out, m->kcache + (size_t)layer * n, n * sizeof(float));
   memcpy(v_out, m->vcache + (size_t)layer * n, n * sizeof(float));
+  return 0;
+}
+
+/* Benchmark aid: fill K/V of positions [0, n_pos) in every layer with seeded N(0,1)-shaped
+ * values (a cheap xorshift sum of uniforms), so that decode steps from position n_pos on read as
+ * many cached positions as after a real prompt of that length, without its prefill.  The
+ * values are not a model's; only the amount of attention work is. */
+int orc_model_prime_cache(orc_model* m, int n_pos, uint64_t seed) {
+  const orc_model_cfg* c = &m->cfg;
+  if (!m->kcache || n_pos < 0 || n_pos > m->max_pos) return -1;
+  const size_t row = (size_t)c->head_dim;
+  for (int l = 0; l < c->n_layers; l++)
+    for (int g = 0; g < c->n_kv_heads; g++)
+      for (int p = 0; p < n_pos; p++) {
+        const size_t off = (((size_t)l * c->n_kv_heads + g) * m->max_pos + p) * row;
+        for (size_t d = 0; d < row; d++) {
+          float kv[2];
+          for (int j = 0; j < 2; j++) {
+            float s = 0.f;
+            for (int u = 0; u < 3; u++) {
+              seed ^= seed << 13; seed ^= seed >> 7; seed ^= seed << 17;
+              s += (float)(seed >> 40) * (1.f / 16777216.f);
+            }
+            kv[j] = (s - 1.5f) * 2.f;
+          }
+          m->kcache[off + d] = m->kv_f16 ? orc_fp16_to_f32(orc_f32_to_fp16(kv[0])) : kv[0];
+          m->vcache[off + d] = m->kv_f16 ? orc_fp16_to_f32(orc_f32_to_fp16(kv[1])) : kv[1];
+        }
+      }
   return 0;
 }
 

@@ -21,7 +21,10 @@
  *   rmsnorm / silu / rope     closed forms (constant vector, 0, pos=0, pair norm)   PINNED
  *   attention                 single position (o=v), uniform scores (o=mean V)      PINNED
  *   argmax                    crafted ties (last index wins), NaN order             PINNED
- *   llama forward             prefix-reuse == full recompute; batched == stepwise   PINNED (invariants)
+ *   llama forward             closed forms with zeroed branches (residual rows =
+ *                             embedding; x + Wo.repeat_kv(Wv.n(x)); x + W2.(silu(W1.n').W3.n');
+ *                             logits from the last position), prefix reuse == full
+ *                             recompute, batched == stepwise (tests/test_oracle_model.py)  PINNED
  *   candle's exact f32 summation order (gemm crate, rayon chunks)                   parity unpinned
  */
 #ifndef TPT_ORACLE_H
@@ -79,7 +82,8 @@ void orc_rope_tables(int rope_dim, float freq_base, int n_pos, float* cos_t, flo
 /* candle_nn::rotary_emb::rope_i for one position over n_heads heads of hd (in place) */
 void orc_rope_i(float* x, int n_heads, int hd, const float* cos_row, const float* sin_row);
 /* decode attention for one query position over L cached positions (f32 cache, layout
- * [Nkv][L_stride][hd]); q [Nq][hd] -> o [Nq][hd].  candle: repeat_kv + matmul + softmax + matmul */
+ * [Nkv][L_stride][hd]); q [Nq][hd] -> o [Nq][hd].  candle: repeat_kv + matmul + softmax + matmul,
+ * the products as fused multiply-adds (the gemm crate on an FMA host) */
 void orc_attention(const float* q, const float* kc, const float* vc, int nq, int nkv, int hd,
                    int L, int L_stride, float* o);
 /* candle LogitsProcessor::sample_argmax: max_by(total_cmp), last index wins on ties */
@@ -98,11 +102,11 @@ orc_model* orc_model_open(const char* gguf_path, char* err, int errlen);
 void orc_model_close(orc_model* m);
 void orc_model_get_cfg(const orc_model* m, orc_model_cfg* cfg);
 /* kv_f16: 1 rounds cached K/V to fp16 (mirrors the GPU cache), 0 keeps f32 like candle */
-/* The attention dot products as fused multiply-adds (on) or separate multiply and add (off, the
- * default).  candle computes q.k^T and att.v with the gemm crate, which picks FMA kernels at
- * run time on hosts that have FMA (gemm-0.17 x86 dispatch), so both are candle's results on
- * some CPU; the spread between them bounds how closely any other summation order can be
- * expected to track candle on an ill-conditioned model. */
+/* The attention dot products as fused multiply-adds (on, the default: candle's gemm crate on
+ * an FMA host, which is what every x86-64-v3 CPU is) or separate multiply and add (off: the
+ * gemm crate on a host without FMA).  Both are candle's results on some CPU; the spread between
+ * them bounds how closely any other summation order can be expected to track candle on an
+ * ill-conditioned model. */
 int orc_model_set_attn_fma(orc_model* m, int on);
 int orc_model_reset(orc_model* m, int max_pos, int kv_f16);
 /* Batched forward of n tokens at positions pos0..pos0+n-1 (causal); writes last-position
@@ -126,6 +130,9 @@ void orc_set_dot_block_order(int on);
 /* copy of one layer's K and V cache, each [n_kv_heads][max_pos][head_dim] f32 */
 int orc_model_kv(const orc_model* m, int layer, float* k_out, float* v_out);
 int orc_model_last_hidden(const orc_model* m, float* out);
+/* benchmark aid: K/V of positions [0, n_pos) filled with seeded synthetic values (not a model's),
+ * so decode from n_pos reads as many cached positions as after a prompt of that length */
+int orc_model_prime_cache(orc_model* m, int n_pos, uint64_t seed);
 
 /* raw tensor lookup for tests: returns pointer into the mmapped file or NULL */
 const void* orc_model_tensor(const orc_model* m, const char* name, int* type, int64_t* ne0,

@@ -58,6 +58,7 @@ def lib():
         L.orc_model_kv.argtypes = [P, I32, P, P]
         L.orc_model_run_layers.argtypes = [P, P, I32, I32, I32, I32, P, I32]
         L.orc_set_dot_block_order.argtypes = [I32]
+        L.orc_model_prime_cache.argtypes = [P, I32, C.c_uint64]
         L.orc_model_tensor.argtypes = [P, C.c_char_p, P, P, P]
         L.orc_model_tensor.restype = P
         _LIB = L
@@ -241,6 +242,10 @@ class Model:
         k, v = np.empty(shape, np.float32), np.empty(shape, np.float32)
         assert lib().orc_model_kv(self.h, layer, _p(k), _p(v)) == 0
         return k, v
+
+    def prime_cache(self, n_pos, seed=1):
+        """Fill K/V of positions [0, n_pos) with synthetic values (benchmark aid)."""
+        assert lib().orc_model_prime_cache(self.h, n_pos, seed) == 0
 
     def last_hidden(self):
         out = np.empty(self.cfg["embed"], np.float32)

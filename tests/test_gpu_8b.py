@@ -1,0 +1,168 @@
+"""Config 5 on the GPU: the Llama-3 8B-shape random-init Q4_K_M model (32 layers, hidden 4096,
+32/8 heads, head_dim 128, FFN 14336 SwiGLU, vocab 128256, RoPE theta 500000), the model bench.py
+measures.
+
+* Against the oracle (candle's arithmetic), where the oracle finishes in seconds: a 16-token
+  prompt plus 8 teacher-forced greedy steps end to end; layers 0 and 31 on 512 positions through
+  the batched-prefill and the decode-step kernels.
+* At full size (2048-token prompt, 256 greedy tokens), through properties that need no oracle:
+  the batched prefill against one decode step per position, the per-op against the persistent
+  decode step, and run-to-run determinism."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import tpthip
+from tpthip import synth
+
+pytestmark = pytest.mark.gpu
+
+SEED = 20261201  # bench.py's model seed
+NT = min(os.cpu_count() or 1, 16)
+
+
+@pytest.fixture(scope="module")
+def gguf_8b(tmp_path_factory):
+    path = str(tmp_path_factory.mktemp("m8b") / "llama3-8b-shape-q4_k_m.gguf")
+    synth.write_llama(path, synth.LLAMA_8B, seed=SEED, nthreads=NT)
+    yield path
+    os.remove(path)
+
+
+def _forced(path, prompt, toks, fma=True, block_order=False):
+    om = oracle.Model(path)
+    try:
+        om.set_attn_fma(fma)
+        oracle.set_dot_block_order(block_order)
+        om.reset(len(prompt) + len(toks) + 1, kv_f16=False)
+        out = [om.forward(prompt, 0, NT)]
+        for i, t in enumerate(toks[:-1]):
+            out.append(om.forward([t], len(prompt) + i, NT))
+        return np.stack(out)
+    finally:
+        oracle.set_dot_block_order(False)
+        om.close()
+
+
+def _margin(l):
+    top = np.sort(l)[-2:]
+    return float(top[1] - top[0])
+
+
+@pytest.mark.timeout(900)
+def test_8b_teacher_forced_short(ctx, gguf_8b):
+    """16 prompt tokens then the oracle's 8 greedy tokens, teacher-forced, f32 cache (candle's).
+    Bar as at the 1B shape: S = the largest max-abs logit distance between the oracle and the
+    oracle under the other plausible candle summation orders (attention without FMA; block-
+    reduced k-quant dots); every step within S, and the same greedy token wherever the oracle's
+    top-two margin exceeds S."""
+    prompt = [int(t) for t in np.random.default_rng(SEED).integers(0, 128256, 16)]
+    om = oracle.Model(gguf_8b)
+    try:
+        toks, _ = om.greedy(prompt, 8, kv_f16=False, nthreads=NT)
+    finally:
+        om.close()
+    ref = _forced(gguf_8b, prompt, toks)
+    spread = np.maximum(np.abs(_forced(gguf_8b, prompt, toks, fma=False) - ref).max(axis=1),
+                        np.abs(_forced(gguf_8b, prompt, toks, block_order=True) - ref).max(axis=1))
+    S = float(spread.max())
+    m = tpthip.Model(ctx, gguf_8b, max_ctx=64, kv_type=tpthip.TYPE_F32)
+    try:
+        nxt, lg = m.prefill(prompt, 0, logits=True)
+        got, gtok = [lg], [nxt]
+        for i, t in enumerate(toks[:-1]):
+            nxt, lg = m.decode_step(t, len(prompt) + i, logits=True)
+            got.append(lg)
+            gtok.append(nxt)
+    finally:
+        m.close()
+    dev = np.abs(np.stack(got) - ref).max(axis=1)
+    margins = [_margin(l) for l in ref]
+    print(f"8B teacher-forced: gpu-oracle max-abs per step {np.round(dev, 4).tolist()}; oracle "
+          f"spread per step {np.round(spread, 4).tolist()}; margins {np.round(margins, 3).tolist()}")
+    assert dev.max() <= S, (dev.max(), S)
+    for i in range(len(toks)):
+        if margins[i] > S:
+            assert gtok[i] == toks[i], i
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("layer", [0, 31])
+def test_8b_layer_vs_oracle(ctx, gguf_8b, layer):
+    """One decoder layer at the 8B shape over 512 positions, both sides fed the same residual
+    rows (layer 0: the embedding rows of random tokens; layer 31: N(0,1) rows), f32 cache: the
+    batched prefill kernels (MFMA GEMMs, matrix-core causal attention over 512 positions) and
+    the decode-step kernels against the oracle.  On identical inputs only f32 rounding differs,
+    which a Q8_K value can turn into a one-step rounding flip that attention carries to later
+    positions: relative L2 over the layer output <= 1e-2, the 1B shape's bar."""
+    T = 512
+    rng = np.random.default_rng(layer)
+    om = oracle.Model(gguf_8b)
+    try:
+        if layer == 0:
+            t, _, _, raw = om.tensor("token_embd.weight")
+            rb = oracle.row_bytes(t, 4096)
+            ids = rng.integers(0, 128256, T)
+            x = np.stack([oracle.dequant(t, raw[i * rb:(i + 1) * rb], 4096) for i in ids])
+        else:
+            x = rng.standard_normal((T, 4096)).astype(np.float32)
+        om.reset(T + 1, kv_f16=False)
+        want = om.run_layers(x, 0, layer, layer + 1, NT)
+    finally:
+        om.close()
+    m = tpthip.Model(ctx, gguf_8b, max_ctx=T + 1, kv_type=tpthip.TYPE_F32)
+    try:
+        errs = {p: float(np.linalg.norm(m.run_layers(x, 0, layer, layer + 1, path=p) - want) /
+                         np.linalg.norm(want)) for p in (0, 1)}
+    finally:
+        m.close()
+    print(f"8B layer {layer}, {T} positions: rel-l2 batched {errs[0]:.2e}, steps {errs[1]:.2e}")
+    assert max(errs.values()) < 1e-2, errs
+
+
+@pytest.mark.timeout(900)
+def test_8b_full_size_properties(ctx, gguf_8b):
+    """The benchmark's workload (2048-token seeded prompt, then 256 greedy tokens, fp16 cache):
+    * the batched prefill and one decode step per position compute the same Q8_K integer
+      products in another f32 order: last-position logits within 5% relative L2 (a wrong layer,
+      position or cache row moves them by ~100%) and the same greedy token when the top-two
+      margin is clear of their distance;
+    * decoding is deterministic: the same prefill + 256 greedy steps twice give the same tokens
+      and bit-identical final logits;
+    * the persistent decode step, where the shape has one, gives the per-op path's tokens."""
+    prompt = [int(t) for t in np.random.default_rng(SEED).integers(0, 128256, 2048)]
+    m = tpthip.Model(ctx, gguf_8b, max_ctx=2048 + 257)
+    os.environ["TPT_HIP_PREFILL"] = "steps"
+    try:
+        ms = tpthip.Model(ctx, gguf_8b, max_ctx=2048 + 257)
+    finally:
+        del os.environ["TPT_HIP_PREFILL"]
+    try:
+        nb, lb = m.prefill(prompt, 0, logits=True)
+        ns, ls = ms.prefill(prompt, 0, logits=True)
+        rel = float(np.linalg.norm(lb - ls) / np.linalg.norm(ls))
+        dmax = float(np.abs(lb - ls).max())
+        print(f"8B 2048-token prompt: batched vs steps rel-l2 {rel:.2e}, max-abs {dmax:.4f}, "
+              f"margin {_margin(ls):.4f}, logit std {float(ls.std()):.3f}")
+        assert rel < 0.05
+        if _margin(ls) > 2 * dmax:
+            assert nb == ns
+        runs = []
+        for _ in range(2):
+            first = m.prefill(prompt, 0)
+            toks = m.decode_greedy(first, len(prompt), 256)
+            _, last = m.decode_step(toks[-1], len(prompt) + 256, logits=True)
+            runs.append((first, toks, last))
+        assert runs[0][0] == runs[1][0] and runs[0][1] == runs[1][1] and len(runs[0][1]) == 256
+        assert np.array_equal(runs[0][2], runs[1][2])
+        try:
+            m.decode_path = m.DECODE_PERSISTENT
+        except tpthip.TptError:
+            return  # no persistent kernel for this shape
+        first = m.prefill(prompt, 0)
+        assert m.decode_greedy(first, len(prompt), 256) == runs[0][1]
+    finally:
+        m.close()
+        ms.close()

@@ -111,6 +111,31 @@ def test_prefix_prefill_equals_full(tiny_model):
     assert full == part
 
 
+def test_kv_cache_matches_oracle(tiny_model, tiny_oracle, kv):
+    """The K/V rows the prompt and 10 decode steps append, read back with tpt_model_kv_read,
+    against the oracle's cache fed the same tokens: layout [kv head][position][head_dim], K after
+    RoPE, V as projected.  f32 cache: within f32 rounding of the GEMV's summation order; fp16
+    cache: the oracle's fp16-rounded values, at most one fp16 ulp apart where an f32 ordering
+    difference moves a value across a rounding boundary."""
+    n = len(PROMPT)
+    first = tiny_model.prefill(PROMPT, 0)
+    toks = [first] + tiny_model.decode_greedy(first, n, 10)[:9]  # fed at positions n .. n+9
+    tiny_oracle.reset(64, kv_f16=(kv == "f16"))
+    tiny_oracle.forward(PROMPT, 0)
+    for i, t in enumerate(toks):
+        tiny_oracle.forward([t], n + i)
+    L = n + len(toks)
+    for layer in range(2):
+        for g, o in zip(tiny_model.kv(layer), tiny_oracle.kv(layer)):
+            g, o = g[:, :L], o[:, :L]
+            if kv == "f32":
+                assert np.linalg.norm(g - o) / np.linalg.norm(o) < 1e-5, layer
+            else:
+                ulp = np.spacing(np.abs(o).astype(np.float16)).astype(np.float32)
+                d = np.abs(g - o)
+                assert np.all(d <= ulp) and np.mean(d > 0) < 0.01, (layer, float((d / ulp).max()))
+
+
 def test_context_bounds(tiny_model):
     with pytest.raises(tpthip.TptError) as e:
         tiny_model.prefill([1, 2], 255)
@@ -207,6 +232,22 @@ def test_engine_prefix_reuse(engine, tiny_oracle):
     # identical prompt again: everything cached, the last position is recomputed
     toks2 = run(engine, tpthip.greedy_params(turn2, 8))
     assert toks2 == ref and engine.last_stats.cached_prefix == len(turn2) - 1
+
+
+def test_engine_reset_cache(engine, tiny_oracle):
+    """KvCache::reset through the engine (the reference's test_reset_clears_tokens,
+    wgpu_kvcache.rs:126-132): after tpt_engine_reset_cache nothing of the previous turn is
+    reusable, the next infer recomputes the whole prompt, and its output is still candle's."""
+    engine.reset_cache()
+    first = run(engine, tpthip.greedy_params(PROMPT, 6))
+    assert engine.cached_prefix_len(PROMPT + first) == len(PROMPT) + 6  # every emitted token was fed
+    engine.reset_cache()
+    assert engine.cached_prefix_len(PROMPT + first) == 0
+    assert engine.cached_prefix_len(PROMPT) == 0
+    again = run(engine, tpthip.greedy_params(PROMPT, 6))
+    assert engine.last_stats.cached_prefix == 0 and engine.last_stats.prompt_tokens == len(PROMPT)
+    ref, _ = tiny_oracle.greedy(PROMPT, 6)
+    assert again == first == ref
 
 
 def test_engine_repeat_penalty_path(engine, tiny_oracle):
@@ -531,29 +572,109 @@ def test_1b_layers_teacher_forced(ctx, gguf_1b, kv):
         assert max(v) < tol, (k, v)
 
 
-@pytest.mark.timeout(900)
-def test_1b_end_to_end_within_candle_spread(ctx, gguf_1b, kv):
-    """End to end at the 1B shape (128-token prompt, then greedy decode).  This random-init
-    model amplifies rounding: candle's own result moves by the same order when its attention
-    products switch between fused and separate multiply-adds (the gemm crate picks per host
-    CPU), and greedy sequences of the two diverge within a few tokens.  So the bar here is that
-    spread: the GPU's last-position logits stay within twice the oracle's FMA/non-FMA distance,
-    and the first greedy token (which the spread does not move) is identical."""
-    logits, _, tok, _, _ = oracle_trace_1b(gguf_1b, kv)
-    om = oracle.Model(gguf_1b)
-    om.set_attn_fma(True)
-    om.reset(256, kv_f16=(kv == "f16"))
-    alt = om.forward(PROMPT_1B, 0, min(os.cpu_count() or 1, 16))
-    om.close()
-    spread = float(np.abs(alt - logits).max())
-    m = tpthip.Model(ctx, gguf_1b, max_ctx=256, kv_type=KV_TYPE[kv])
+def _forced_logits(path, prompt, toks, fma=True, block_order=False, nthreads=16):
+    """Oracle logits at every step of a teacher-forced run (f32 cache, candle's): step 0 after
+    the prompt, step i after feeding toks[i-1]."""
+    om = oracle.Model(path)
     try:
-        first, lg = m.prefill(PROMPT_1B, 0, logits=True)
-        dev = float(np.abs(lg - logits).max())
-        print(f"gpu-oracle {dev:.3f}, oracle fma-nonfma spread {spread:.3f}")
-        assert first == tok == oracle.argmax(alt)
-        assert dev < 2 * spread + 1e-2
-        toks = m.decode_greedy(first, len(PROMPT_1B), 31)
-        assert len(toks) == 31 and all(0 <= t < 128256 for t in toks)
+        om.set_attn_fma(fma)
+        oracle.set_dot_block_order(block_order)
+        om.reset(len(prompt) + len(toks) + 1, kv_f16=False)
+        out = [om.forward(prompt, 0, nthreads)]
+        for i, t in enumerate(toks[:-1]):
+            out.append(om.forward([t], len(prompt) + i, nthreads))
+        return np.stack(out)
+    finally:
+        oracle.set_dot_block_order(False)
+        om.close()
+
+
+def _margin(l):
+    top = np.sort(l)[-2:]
+    return float(top[1] - top[0])
+
+
+@pytest.mark.timeout(1200)
+def test_1b_teacher_forced_decode(ctx, gguf_1b):
+    """Config 1 end to end against candle's arithmetic: the 128-token prompt, then the 128 greedy
+    tokens of the oracle's own run (candle_engine.rs:269-324), teacher-forced into both sides,
+    f32 cache (candle's).  The oracle's summation order inside candle's dot products is unpinned,
+    and this random-init model amplifies any order change (a Q8_K activation value that rounds
+    the other way moves the next layer), so the bar is the oracle's own spread S: the largest
+    max-abs logit distance, over all 128 steps, between the oracle and the oracle run with the
+    other two plausible candle orders (separate multiply-adds in attention, as the gemm crate on a
+    host without FMA; block-reduced k-quant dot products).  Every step: GPU logits within S of
+    the oracle, and the GPU's greedy token equal to the oracle's wherever the oracle's top-two
+    margin exceeds S (a margin below S is a token candle itself could pick either way).  Then
+    free-running: the GPU's greedy tokens equal the oracle's up to the first such close step, and
+    over at least the first 32 tokens when no close step comes earlier."""
+    nt = min(os.cpu_count() or 1, 16)
+    om = oracle.Model(gguf_1b)
+    try:
+        ref_toks, _ = om.greedy(PROMPT_1B, 128, kv_f16=False, nthreads=nt)
+    finally:
+        om.close()
+    ref = _forced_logits(gguf_1b, PROMPT_1B, ref_toks, nthreads=nt)
+    alt_fma = _forced_logits(gguf_1b, PROMPT_1B, ref_toks, fma=False, nthreads=nt)
+    alt_blk = _forced_logits(gguf_1b, PROMPT_1B, ref_toks, block_order=True, nthreads=nt)
+    spread = np.maximum(np.abs(alt_fma - ref).max(axis=1), np.abs(alt_blk - ref).max(axis=1))
+    S = float(spread.max())
+    m = tpthip.Model(ctx, gguf_1b, max_ctx=512, kv_type=tpthip.TYPE_F32)
+    try:
+        nxt, lg = m.prefill(PROMPT_1B, 0, logits=True)
+        got, gtok = [lg], [nxt]
+        for i, t in enumerate(ref_toks[:-1]):
+            nxt, lg = m.decode_step(t, len(PROMPT_1B) + i, logits=True)
+            got.append(lg)
+            gtok.append(nxt)
+        got = np.stack(got)
+        first = m.prefill(PROMPT_1B, 0)
+        free = [first] + m.decode_greedy(first, len(PROMPT_1B), 127)
     finally:
         m.close()
+    dev = np.abs(got - ref).max(axis=1)
+    margins = np.array([_margin(l) for l in ref])
+    close = margins <= S
+    print(f"1B teacher-forced, 128 steps: gpu-oracle max-abs logits max {dev.max():.4f} "
+          f"median {np.median(dev):.4f}; oracle spread S {S:.4f} (per step median "
+          f"{np.median(spread):.4f}); logit std {float(ref.std()):.3f}; steps with top-2 margin "
+          f"<= S: {int(close.sum())} {np.flatnonzero(close).tolist()}; tokens equal where gated-in: "
+          f"{int(sum(g == r for g, r, c in zip(gtok, ref_toks, close) if not c))}/{int((~close).sum())}")
+    assert dev.max() <= S, (dev.max(), S)
+    for i in np.flatnonzero(~close):
+        assert gtok[i] == ref_toks[i], (i, gtok[i], ref_toks[i], margins[i])
+    n_ok = int(np.flatnonzero(close)[0]) if close.any() else 128
+    assert free[:n_ok] == ref_toks[:n_ok]
+    if n_ok >= 32:
+        assert free[:32] == ref_toks[:32]
+
+
+@pytest.mark.timeout(900)
+def test_1b_kv_cache_matches_oracle(ctx, gguf_1b, kv):
+    """K/V cache contents after the 128-token prompt, read back with tpt_model_kv_read, against
+    the oracle's cache (the same mode's element type): layout [kv head][position][head_dim] with
+    RoPE applied to K; layer 0 (identical inputs: the embedding rows) to f32 rounding of the
+    GEMV, every layer within the per-layer bar of test_1b_layers_teacher_forced; positions past
+    the prompt untouched (zero)."""
+    om = oracle.Model(gguf_1b)
+    m = tpthip.Model(ctx, gguf_1b, max_ctx=256, kv_type=KV_TYPE[kv])
+    try:
+        om.reset(256, kv_f16=(kv == "f16"))
+        om.forward(PROMPT_1B, 0, min(os.cpu_count() or 1, 16))
+        m.prefill(PROMPT_1B, 0)
+        n = len(PROMPT_1B)
+        worst = []
+        for layer in range(16):
+            gk, gv = m.kv(layer)
+            ok, ov = om.kv(layer)
+            for g, o in ((gk, ok), (gv, ov)):
+                g = g.astype(np.float32)
+                assert g.shape == o.shape == (8, 256, 64)
+                assert not np.any(g[:, n:]), "positions past the prompt were written"
+                e = _rel_l2(g[:, :n], o[:, :n])
+                worst.append(e)
+                assert e < (1e-5 if layer == 0 else (1e-2 if kv == "f32" else 2e-2)), (layer, e)
+        print(kv, "kv rel-l2 per layer (K, V):", " ".join(f"{e:.1e}" for e in worst))
+    finally:
+        m.close()
+        om.close()

@@ -192,7 +192,7 @@ def test_attention_gqa_hd128(ctx, L):
     assert rel_l2(o, ref) < 1e-5
 
 
-@pytest.mark.parametrize("L", [1, 2, 17, 512, 4096, 16384])
+@pytest.mark.parametrize("L", [1, 2, 17, 512, 4096, 16384, 32768])
 def test_attention_mha_hd96(ctx, L):
     o, ref = attention_case(ctx, 32, 32, 96, L, seed=L + 1)
     assert rel_l2(o, ref) < 1e-5

@@ -63,11 +63,113 @@ def test_new_tokens_shorter_than_cached():
     assert tpthip.common_prefix_len([1, 2, 3, 4, 5], [1, 2, 3]) == 3
 
 
-def test_reset_clears_tokens():
-    # KvCache::reset empties the record: afterwards nothing is reusable
-    cached = [1, 2, 3]
-    cached.clear()
-    assert tpthip.common_prefix_len(cached, [1, 2, 3]) == 0
+# test_reset_clears_tokens (wgpu_kvcache.rs:126-132) drives the engine's KvCache::reset
+# equivalent, tpt_engine_reset_cache, so it needs a device: tests/test_gpu_model.py.
+
+
+# ---- GGUF validation without a device (tpt_model_inspect: extract_meta + the loader's checks)
+
+@pytest.fixture(scope="module")
+def tiny_file(tmp_path_factory):
+    p = str(tmp_path_factory.mktemp("gguf") / "tiny.gguf")
+    synth.write_llama(p, synth.TINY, seed=3)
+    return p
+
+
+def test_inspect_reads_the_metadata(tiny_file):
+    d = tpthip.inspect_gguf(tiny_file)
+    assert d["architecture"] == "llama"
+    assert (d["n_layers"], d["embed"], d["n_heads"], d["n_kv_heads"], d["head_dim"], d["ffn"],
+            d["vocab"], d["context_length"]) == (2, 256, 4, 2, 64, 512, 1024, 512)
+    assert abs(d["rope_base"] - 500000.0) < 1 and abs(d["rms_eps"] - 1e-5) < 1e-9
+    assert d["type_q"] == tpthip.TYPE_Q4_K and d["type_out"] == tpthip.TYPE_Q6_K
+    # weight bytes: every tensor once; a decode step reads every layer tensor, the LM head,
+    # the final norm and one embedding row
+    from gguf_edit import Gguf
+    g = Gguf(tiny_file)
+    size = {t["name"]: int(np.prod(t["ne"])) // tpthip.BLOCK[t["type"]] * tpthip.TYPE_SIZE[t["type"]]
+            for t in g.tensors}
+    assert d["weight_bytes"] == sum(size.values())
+    emb_row = 256 // 256 * tpthip.TYPE_SIZE[tpthip.TYPE_Q6_K]
+    assert d["decode_bytes_per_token"] == sum(size.values()) - size["token_embd.weight"] + emb_row
+
+
+def _bad(tiny_file, tmp_path, edit):
+    from gguf_edit import Gguf
+    g = Gguf(tiny_file)
+    edit(g)
+    return g.write(str(tmp_path / "bad.gguf"))
+
+
+def _expect(path, code, text):
+    with pytest.raises(tpthip.TptError) as e:
+        tpthip.inspect_gguf(path)
+    assert e.value.code == code and text in str(e.value), str(e.value)
+
+
+def test_inspect_rewritten_file_is_valid(tiny_file, tmp_path):
+    # the editor round-trips: an unchanged rewrite still validates
+    assert tpthip.inspect_gguf(_bad(tiny_file, tmp_path, lambda g: None))["n_layers"] == 2
+
+
+def test_inspect_rejects_zero_extent(tiny_file, tmp_path):
+    # [256, 256, 0]: zero bytes; the kernels would read 256 rows past it
+    def edit(g):
+        g.tensor("blk.0.attn_q.weight")["ne"] = [256, 256, 0]
+    _expect(_bad(tiny_file, tmp_path, edit), tpthip.ERR_FORMAT, "unexpected shape")
+
+
+def test_inspect_rejects_extra_dimensions(tiny_file, tmp_path):
+    def edit(g):
+        g.tensor("blk.1.ffn_down.weight")["ne"] = [512, 128, 2]
+    _expect(_bad(tiny_file, tmp_path, edit), tpthip.ERR_FORMAT, "unexpected shape")
+
+
+def test_inspect_rejects_huge_extent(tiny_file, tmp_path):
+    def edit(g):
+        g.tensor("blk.0.attn_k.weight")["ne"] = [256, 1 << 41]
+    _expect(_bad(tiny_file, tmp_path, edit), tpthip.ERR_FORMAT, "extent out of range")
+
+
+def test_inspect_rejects_overflowing_element_count(tiny_file, tmp_path):
+    # each extent below 2^40, the product past 2^62
+    def edit(g):
+        g.tensor("blk.0.attn_k.weight")["ne"] = [256, (1 << 39) + 1, 1 << 30]
+    _expect(_bad(tiny_file, tmp_path, edit), tpthip.ERR_FORMAT, "too many elements")
+
+
+def test_inspect_rejects_wrapping_offset(tiny_file, tmp_path):
+    # data offset + tensor offset wraps past 2^64 onto a small address
+    def edit(g):
+        g.tensor("output_norm.weight")["offset"] = (1 << 64) - 64
+    _expect(_bad(tiny_file, tmp_path, edit), tpthip.ERR_FORMAT, "past end of file")
+
+
+def test_inspect_rejects_tensor_past_eof(tiny_file, tmp_path):
+    def edit(g):
+        t = g.tensor("blk.1.ffn_up.weight")
+        t["offset"] = len(g.data) - 100
+    _expect(_bad(tiny_file, tmp_path, edit), tpthip.ERR_FORMAT, "past end of file")
+
+
+def test_inspect_rejects_wrong_row_length(tiny_file, tmp_path):
+    def edit(g):
+        g.tensor("blk.0.ffn_gate.weight")["ne"] = [512, 256]
+    _expect(_bad(tiny_file, tmp_path, edit), tpthip.ERR_FORMAT, "unexpected shape")
+
+
+def test_inspect_rejects_unsupported_matrix_type(tiny_file, tmp_path):
+    # ggml type 3 (Q4_1): a block type this engine does not read
+    def edit(g):
+        g.tensor("blk.0.attn_v.weight")["type"] = 3
+    _expect(_bad(tiny_file, tmp_path, edit), tpthip.ERR_UNSUPPORTED, "does not read")
+
+
+def test_inspect_missing_file_and_bad_magic(tiny_file, tmp_path):
+    _expect(str(tmp_path / "none.gguf"), tpthip.ERR_IO, "opening")
+    p = str(tmp_path / "magic.gguf")
+    open(p, "wb").write(b"GGUX" + open(tiny_file, "rb").read()[4:])
+    _expect(p, tpthip.ERR_FORMAT, "bad magic")
 
 
 # ---- workload generator

@@ -155,14 +155,24 @@ int GgufFile::open(const std::string& p) {
   if (get_u64("general.alignment", &a) && a > 0 && (a & (a - 1)) == 0) align = a;
   const uint64_t pos = (uint64_t)(r.p - map);
   data_offset = (pos + align - 1) / align * align;
+  if (data_offset > size) return fail(TPT_ERR_FORMAT, "GGUF data section starts past end of file");
+  const uint64_t data_bytes = size - data_offset;
   for (GgufTensor& t : tensors) {
-    const int64_t n = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
+    // every extent in [0, 2^40) and the element count below 2^62: no product can overflow
+    uint64_t n = 1;
+    for (int d = 0; d < 4; d++) {
+      if (t.ne[d] < 0 || t.ne[d] >= ((int64_t)1 << 40))
+        return fail(TPT_ERR_FORMAT, "tensor '" + t.name + "' has an extent out of range");
+      const uint64_t e = (uint64_t)t.ne[d];
+      if (e && n > (((uint64_t)1 << 62) / e)) return fail(TPT_ERR_FORMAT, "tensor '" + t.name + "' has too many elements");
+      n *= e;
+    }
     const int bs = type_block(t.type), tb = type_bytes(t.type);
     if (tb == 0) continue;  // a dtype this path never reads: left unmapped, rejected if used
-    if (n < 0 || n % bs) return fail(TPT_ERR_FORMAT, "tensor '" + t.name + "' size is not a whole number of blocks");
-    t.bytes = (size_t)(n / bs) * (size_t)tb;
-    // wgpu_loader.rs:130-132
-    if (data_offset + t.offset + t.bytes > size)
+    if (n % (uint64_t)bs) return fail(TPT_ERR_FORMAT, "tensor '" + t.name + "' size is not a whole number of blocks");
+    t.bytes = (size_t)(n / (uint64_t)bs) * (size_t)tb;
+    // wgpu_loader.rs:130-132, written so that no sum can wrap
+    if (t.offset > data_bytes || t.bytes > data_bytes - t.offset)
       return fail(TPT_ERR_FORMAT, "tensor '" + t.name + "' extends past end of file");
     t.data = map + data_offset + t.offset;
   }

@@ -891,6 +891,18 @@ int decode_layers_plan(const tpt_ctx* ctx, DecodeArgs& a) {
   const size_t mrg = 2 * 4 * (size_t)a.n_chunks;
   const size_t lds = (std::max(std::max(emb, att), mrg) + 15) & ~(size_t)15;
   if (lds > (size_t)kMaxLds) return fail(TPT_ERR_UNSUPPORTED, "decode layers: LDS budget exceeded");
+  // The grid barriers need every workgroup resident at once: one per compute unit must fit
+  // with this LDS size and the instantiation's registers.  (Work of other streams or processes
+  // can still hold compute units; the barrier's bounded wait then reports an error.)
+  int per_cu = 0;
+#define TPT_OCC(KVT, KT, HD, G, BH, BF, RBF)                                                      \
+  if (a.kv_type == KVT && a.hd == HD && g == G && bh == BH && bf == BF && rbf == RBF)              \
+    TPT_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(                                         \
+        &per_cu, (const void*)decode_layers_kernel<KT, HD, G, BH, BF, RBF>, NT, lds));
+  TPT_DECODE_CFGS(TPT_OCC)
+#undef TPT_OCC
+  if ((long)per_cu * grid < grid)
+    return fail(TPT_ERR_UNSUPPORTED, "decode layers: a workgroup per compute unit cannot be resident");
   a.lds = (int)lds;
   return TPT_OK;
 }

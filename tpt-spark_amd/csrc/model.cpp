@@ -57,17 +57,18 @@ tpt_model::~tpt_model() {
   if (ids_host) (void)hipHostFree(ids_host);
 }
 
-int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_type,
-                    tpt_progress_fn progress, void* user) {
-  if (kv_type != TPT_TYPE_F16 && kv_type != TPT_TYPE_F32)
-    return fail(TPT_ERR_UNSUPPORTED, "KV cache type must be F16 or F32");
-  ctx = c;
-  stream = c->stream;
-  path = gguf_path;
-  GgufFile f;
-  int rc = f.open(gguf_path);
-  if (rc) return rc;
+// Metadata and tensor table of a Llama GGUF, validated for this engine: extract_meta's keys and
+// defaults (wgpu_loader.rs:305-406), the architecture check of CandleEngine::load
+// (candle_engine.rs:146-156), and every tensor the forward pass reads present with the shape,
+// type and byte size its kernels assume.  Host only: nothing touches a device.
+struct ModelTensors {
+  struct LT { const GgufTensor *q, *k, *v, *o, *g, *u, *d, *an, *fn; };
+  std::vector<LT> lt;
+  const GgufTensor *te = nullptr, *to = nullptr, *ton = nullptr;
+};
 
+static int read_model_meta(const GgufFile& f, tpt_model_desc& desc, ModelTensors& mt) {
+  int rc;
   // ---- metadata (extract_meta, wgpu_loader.rs:305-406; arch check as CandleEngine::load,
   //      candle_engine.rs:146-156: the Llama-dense families this engine implements)
   std::string arch = "llama";
@@ -87,6 +88,8 @@ int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_t
   desc.rope_base = f.get_f32(a + ".rope.freq_base", &fv) ? fv : 10000.f;
   desc.rms_eps = f.get_f32(a + ".attention.layer_norm_rms_epsilon", &fv) ? fv : 1e-5f;
   desc.rope_scale = 1.f;  // candle's quantized_llama applies no RoPE scaling
+  if (desc.n_layers < 1 || desc.n_layers > 4096 || desc.embed < 1)
+    return fail(TPT_ERR_FORMAT, "block_count / embedding_length out of range in GGUF metadata");
   if (desc.n_heads <= 0 || desc.n_kv_heads <= 0 || desc.embed % desc.n_heads || desc.n_heads % desc.n_kv_heads)
     return fail(TPT_ERR_FORMAT, "inconsistent head counts in GGUF metadata");
   desc.head_dim = desc.embed / desc.n_heads;
@@ -102,12 +105,17 @@ int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_t
     if (!t) return fail(TPT_ERR_FORMAT, "missing tensor " + name);
     if (type_bytes(t->type) == 0 || !t->data)
       return fail(TPT_ERR_UNSUPPORTED, "tensor " + name + " has ggml type " + std::to_string(t->type) + ", which engine-hip does not read");
-    if (t->ne[0] != ne0 || (ne1 >= 0 && t->ne[1] != ne1))
+    // a matrix [ne1][ne0] or a vector [ne0]: higher extents 1, at least one row, and exactly the
+    // bytes the kernels read (ne1 rows of ne0 elements), so no kernel reads past the tensor
+    if (t->n_dims > 2 || t->ne[2] != 1 || t->ne[3] != 1 || t->ne[0] != ne0 || t->ne[1] < 1 ||
+        (ne1 >= 0 && t->ne[1] != ne1))
       return fail(TPT_ERR_FORMAT, "tensor " + name + " has an unexpected shape");
+    if (t->bytes != (size_t)t->ne[1] * row_bytes(t->type, (int)ne0))
+      return fail(TPT_ERR_FORMAT, "tensor " + name + " has an unexpected byte size");
     *out = t;
     return TPT_OK;
   };
-  const GgufTensor *te, *to = nullptr, *ton;
+  const GgufTensor *&te = mt.te, *&to = mt.to, *&ton = mt.ton;
   if ((rc = need("token_embd.weight", H, -1, &te))) return rc;
   desc.vocab = (int)te->ne[1];
   if (f.find("output.weight")) {
@@ -123,11 +131,11 @@ int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_t
   uint64_t ffn_meta;
   desc.ffn = f.get_u64(a + ".feed_forward_length", &ffn_meta) ? (int)ffn_meta : (int)g0->ne[1];
 
-  struct LT { const GgufTensor *q, *k, *v, *o, *g, *u, *d, *an, *fn; };
-  std::vector<LT> lt(desc.n_layers);
+  mt.lt.resize(desc.n_layers);
+  std::vector<ModelTensors::LT>& lt = mt.lt;
   for (int l = 0; l < desc.n_layers; l++) {
     const std::string p = "blk." + std::to_string(l) + ".";
-    LT& t = lt[l];
+    ModelTensors::LT& t = lt[l];
     if ((rc = need(p + "attn_q.weight", H, qd, &t.q)) || (rc = need(p + "attn_k.weight", H, kd, &t.k)) ||
         (rc = need(p + "attn_v.weight", H, kd, &t.v)) || (rc = need(p + "attn_output.weight", qd, H, &t.o)) ||
         (rc = need(p + "ffn_gate.weight", H, desc.ffn, &t.g)) || (rc = need(p + "ffn_up.weight", H, desc.ffn, &t.u)) ||
@@ -136,12 +144,41 @@ int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_t
       return rc;
     for (const GgufTensor* m : {t.q, t.k, t.v, t.o, t.g, t.u, t.d})
       if (!matrix_type_ok(m->type))
-        return fail(TPT_ERR_UNSUPPORTED, "tensor " + m->name + " has type " + type_name(m->type) + "; engine-hip reads Q4_K, Q6_K and Q8_0 matrices");
+        return fail(TPT_ERR_UNSUPPORTED, "tensor " + m->name + " has type " + type_name(m->type) + "; engine-hip reads Q4_K, Q5_K, Q6_K, Q8_0 and Q4_0 matrices");
     if (t.an->type != TPT_TYPE_F32 || t.fn->type != TPT_TYPE_F32) return fail(TPT_ERR_UNSUPPORTED, "norm weights must be F32");
     if (t.g->type != t.u->type)
       return fail(TPT_ERR_UNSUPPORTED, "ffn_gate and ffn_up of different types are not supported yet");
     if (H % 256 || desc.ffn % 256 || qd % 256) return fail(TPT_ERR_UNSUPPORTED, "dimensions must be multiples of 256");
   }
+
+  uint64_t step_bytes = 0, total = 0;
+  for (const ModelTensors::LT& t : lt)
+    for (const GgufTensor* m : {t.q, t.k, t.v, t.o, t.g, t.u, t.d, t.an, t.fn}) step_bytes += m->bytes;
+  total = step_bytes + te->bytes + (to != te ? to->bytes : 0) + ton->bytes;
+  desc.weight_bytes = total;
+  desc.decode_bytes_per_token = step_bytes + to->bytes + ton->bytes + row_bytes(te->type, desc.embed);
+  desc.type_q = lt[0].q->type; desc.type_k = lt[0].k->type; desc.type_v = lt[0].v->type;
+  desc.type_o = lt[0].o->type; desc.type_gate = lt[0].g->type; desc.type_up = lt[0].u->type;
+  desc.type_down = lt[0].d->type; desc.type_embd = te->type; desc.type_out = to->type;
+  return TPT_OK;
+}
+
+int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_type,
+                    tpt_progress_fn progress, void* user) {
+  if (kv_type != TPT_TYPE_F16 && kv_type != TPT_TYPE_F32)
+    return fail(TPT_ERR_UNSUPPORTED, "KV cache type must be F16 or F32");
+  ctx = c;
+  stream = c->stream;
+  path = gguf_path;
+  GgufFile f;
+  int rc = f.open(gguf_path);
+  if (rc) return rc;
+  ModelTensors mt;
+  if ((rc = read_model_meta(f, desc, mt))) return rc;
+  const int H = desc.embed, hd = desc.head_dim, nq = desc.n_heads, nkv = desc.n_kv_heads;
+  const int qd = nq * hd;
+  const std::vector<ModelTensors::LT>& lt = mt.lt;
+  const GgufTensor *te = mt.te, *to = mt.to, *ton = mt.ton;
 
   // ---- HBM layout: per layer q|k|v adjacent (one GEMV over qd + 2 kd rows), then the rest
   std::vector<std::pair<const GgufTensor*, size_t>> plan;  // tensor, arena offset
@@ -215,10 +252,9 @@ int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_t
     return nullptr;
   };
   layers.resize(desc.n_layers);
-  uint64_t step_bytes = 0;
   for (int l = 0; l < desc.n_layers; l++) {
     Layer& L = layers[l];
-    const LT& t = lt[l];
+    const ModelTensors::LT& t = lt[l];
     L.q = dev(t.q); L.k = dev(t.k); L.v = dev(t.v); L.o = dev(t.o);
     L.gate = dev(t.g); L.up = dev(t.u); L.down = dev(t.d);
     L.attn_norm = (const float*)dev(t.an);
@@ -226,7 +262,6 @@ int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_t
     L.tq = t.q->type; L.tk = t.k->type; L.tv = t.v->type; L.to = t.o->type;
     L.tg = t.g->type; L.tu = t.u->type; L.td = t.d->type;
     L.qkv_adjacent = L.tq == L.tk && L.tk == L.tv && L.k == L.q + t.q->bytes && L.v == L.k + t.k->bytes;
-    for (const GgufTensor* m : {t.q, t.k, t.v, t.o, t.g, t.u, t.d, t.an, t.fn}) step_bytes += m->bytes;
   }
   embd = dev(te);
   embd_type = te->type;
@@ -234,12 +269,7 @@ int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_t
   out = dev(to);
   out_type = to->type;
   out_norm = (const float*)dev(ton);
-  step_bytes += to->bytes + ton->bytes + embd_row;
   desc.weight_bytes = arena_bytes;
-  desc.decode_bytes_per_token = step_bytes;
-  desc.type_q = lt[0].q->type; desc.type_k = lt[0].k->type; desc.type_v = lt[0].v->type;
-  desc.type_o = lt[0].o->type; desc.type_gate = lt[0].g->type; desc.type_up = lt[0].u->type;
-  desc.type_down = lt[0].d->type; desc.type_embd = te->type; desc.type_out = to->type;
 
   // ---- runtime state
   const int max_ctx = max_ctx_req > 0 ? max_ctx_req : desc.context_length;
@@ -288,8 +318,12 @@ int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_t
         tc[(size_t)p * half + i] = cosf(ang);
         ts[(size_t)p * half + i] = sinf(ang);
       }
-    TPT_HIP(hipMemcpy(rope_cos, tc.data(), tc.size() * 4, hipMemcpyHostToDevice));
-    TPT_HIP(hipMemcpy(rope_sin, ts.data(), ts.size() * 4, hipMemcpyHostToDevice));
+    // on the model stream, behind the clearing of the runtime region (a plain hipMemcpy runs
+    // on the null stream, which does not wait for this non-blocking stream), and complete
+    // before the host tables go out of scope
+    TPT_HIP(hipMemcpyAsync(rope_cos, tc.data(), tc.size() * 4, hipMemcpyHostToDevice, stream));
+    TPT_HIP(hipMemcpyAsync(rope_sin, ts.data(), ts.size() * 4, hipMemcpyHostToDevice, stream));
+    TPT_HIP(hipStreamSynchronize(stream));
   }
   TPT_HIP(hipHostMalloc((void**)&st_host, sizeof(StepState)));
   TPT_HIP(hipHostMalloc((void**)&ids_host, (size_t)max_ctx * 4));
@@ -360,7 +394,8 @@ int tpt_model::setup_decode_layers() {
     t[l].qkv = L.q; t[l].o = L.o; t[l].gate = L.gate; t[l].up = L.up; t[l].down = L.down;
     t[l].attn_norm = L.attn_norm; t[l].ffn_norm = L.ffn_norm;
   }
-  TPT_HIP(hipMemcpy(m + dec_sync_bytes, t.data(), tab, hipMemcpyHostToDevice));
+  TPT_HIP(hipMemcpyAsync(m + dec_sync_bytes, t.data(), tab, hipMemcpyHostToDevice, stream));
+  TPT_HIP(hipStreamSynchronize(stream));
   dec = d;
   int rc = dec_reset();
   if (rc) return rc;
@@ -625,8 +660,8 @@ int tpt_model::prefill_scratch(int T, int n_chunks) {
                o_ids = carve((size_t)T * 4);
   // split-K workspace of the GEMMs (short prompts): the largest splits x T x N over the shapes
   size_t gsplit = 0;
-  for (const int* kn : {(const int[2]){H, qd + 2 * kd}, (const int[2]){qd, H}, (const int[2]){H, F},
-                        (const int[2]){F, H}}) {
+  const int shapes[4][2] = {{H, qd + 2 * kd}, {qd, H}, {H, F}, {F, H}};  // (K, N)
+  for (const auto& kn : shapes) {
     const int ns = gemm_splits(T, kn[1], kn[0]);
     if (ns > 1) gsplit = std::max(gsplit, (size_t)ns * T * kn[1]);
   }
@@ -911,6 +946,18 @@ int tpt_model_load(tpt_ctx* c, const char* gguf_path, int max_ctx, int kv_type,
     return rc;
   }
   *out = m;
+  return TPT_OK;
+}
+
+int tpt_model_inspect(const char* gguf_path, tpt_model_desc* out) {
+  if (!gguf_path || !out) return fail(TPT_ERR_INVALID, "null argument");
+  GgufFile f;
+  int rc = f.open(gguf_path);
+  if (rc) return rc;
+  tpt_model_desc d{};
+  ModelTensors mt;
+  if ((rc = read_model_meta(f, d, mt))) return rc;
+  *out = d;
   return TPT_OK;
 }
 

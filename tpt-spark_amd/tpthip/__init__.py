@@ -83,6 +83,7 @@ EXPORTS = {
     "tpt_argmax": ([P, P, I64, P], I32),
     "tpt_model_load": ([P, C.c_char_p, I32, I32, PROGRESS_FN, P, P], I32),
     "tpt_model_describe": ([P, P], I32),
+    "tpt_model_inspect": ([C.c_char_p, P], I32),
     "tpt_model_destroy": ([P], I32),
     "tpt_model_prefill": ([P, P, I32, I32, P, P], I32),
     "tpt_model_decode_step": ([P, U32, I32, P, P], I32),
@@ -330,6 +331,15 @@ class Context:
         out = C.c_uint32()
         check(lib().tpt_argmax(self.h, buf.ptr, n, C.byref(out)))
         return out.value
+
+
+def inspect_gguf(path):
+    """tpt_model_inspect: the validated metadata of a GGUF, host only (no device needed)."""
+    d = ModelDesc()
+    check(lib().tpt_model_inspect(path.encode(), C.byref(d)))
+    out = {n: getattr(d, n) for n, _ in ModelDesc._fields_}
+    out["architecture"] = d.architecture.decode()
+    return out
 
 
 class Model:
