@@ -79,7 +79,9 @@ def test_8b_teacher_forced_short(ctx, gguf_8b):
     finally:
         m.close()
     dev = np.abs(np.stack(got) - ref).max(axis=1)
+    rel = np.linalg.norm(np.stack(got) - ref, axis=1) / np.linalg.norm(ref, axis=1)
     margins = [_margin(l) for l in ref]
+    print(f"8B teacher-forced: gpu-oracle rel-l2 per step {np.round(rel, 4).tolist()}")
     print(f"8B teacher-forced: gpu-oracle max-abs per step {np.round(dev, 4).tolist()}; oracle "
           f"spread per step {np.round(spread, 4).tolist()}; margins {np.round(margins, 3).tolist()}")
     assert dev.max() <= S, (dev.max(), S)
@@ -126,9 +128,14 @@ def test_8b_layer_vs_oracle(ctx, gguf_8b, layer):
 def test_8b_full_size_properties(ctx, gguf_8b):
     """The benchmark's workload (2048-token seeded prompt, then 256 greedy tokens, fp16 cache):
     * the batched prefill and one decode step per position compute the same Q8_K integer
-      products in another f32 order: last-position logits within 5% relative L2 (a wrong layer,
-      position or cache row moves them by ~100%) and the same greedy token when the top-two
-      margin is clear of their distance;
+      products in another f32 order.  Every matmul requantizes its input to Q8_K, which turns a
+      deviation d far below the quantization step D into about sqrt(d D) (a value crosses a
+      rounding boundary with probability d / D and then moves by D), so two orders drift apart
+      until their distance is of the step's own scale: measured 0.12 relative L2 of the
+      last-position logits here, and about 0.1 between the GPU and the oracle after the 16-token
+      prompt above.  Bar: relative L2 below 0.3 (an uncorrelated vector of the same size, as a
+      wrong layer, position or cache row gives, is at about 1.4), and the same greedy token
+      when the top-two margin is clear of their distance;
     * decoding is deterministic: the same prefill + 256 greedy steps twice give the same tokens
       and bit-identical final logits;
     * the persistent decode step, where the shape has one, gives the per-op path's tokens."""
@@ -146,7 +153,7 @@ def test_8b_full_size_properties(ctx, gguf_8b):
         dmax = float(np.abs(lb - ls).max())
         print(f"8B 2048-token prompt: batched vs steps rel-l2 {rel:.2e}, max-abs {dmax:.4f}, "
               f"margin {_margin(ls):.4f}, logit std {float(ls.std()):.3f}")
-        assert rel < 0.05
+        assert rel < 0.3
         if _margin(ls) > 2 * dmax:
             assert nb == ns
         runs = []

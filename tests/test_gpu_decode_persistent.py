@@ -119,32 +119,37 @@ def test_wide_paths_agree(ctx, wide_gguf, kv, plen):
     assert np.array_equal(lg_p, lg_k)
 
 
-def _oracle_forced(path, prompt, toks, fma):
+def _oracle_forced(path, prompt, toks, fma=True, block_order=False):
     """Oracle logits after feeding each of toks (teacher-forced, f32 cache)."""
     om = oracle.Model(path)
     try:
         om.set_attn_fma(fma)
+        oracle.set_dot_block_order(block_order)
         om.reset(len(prompt) + len(toks) + 1, kv_f16=False)
         om.forward(prompt, 0)
         return [om.forward([t], len(prompt) + i) for i, t in enumerate(toks)]
     finally:
+        oracle.set_dot_block_order(False)
         om.close()
 
 
 def test_wide_persistent_matches_oracle(ctx, wide_gguf):
     """8B-width layers on the persistent path against the oracle (f32 cache, candle's), both
-    fed the oracle's greedy tokens.  This random-init model amplifies rounding (candle's own
-    logits move when its attention products switch between fused and separate multiply-adds),
-    so as at the 1B shape the bar is that spread: the device logits after each of 8 steps stay
-    within twice the oracle's FMA / non-FMA distance (+1e-2)."""
+    fed the oracle's greedy tokens.  This random-init model amplifies rounding (every matmul
+    requantizes its input to Q8_K), so as at the 1B shape the bar is the oracle's own spread S:
+    the largest max-abs distance, over the 8 steps, between the oracle and the oracle under
+    candle's other two plausible summation orders (attention without FMA; block-reduced k-quant
+    dots); the device logits after each step stay within S."""
     prompt = [int(t) for t in np.random.default_rng(5).integers(0, WIDE["vocab"], 40)]
     om = oracle.Model(wide_gguf)
     try:
         toks, _ = om.greedy(prompt, 8, kv_f16=False)
     finally:
         om.close()
-    ref = _oracle_forced(wide_gguf, prompt, toks, False)
-    alt = _oracle_forced(wide_gguf, prompt, toks, True)
+    ref = _oracle_forced(wide_gguf, prompt, toks)
+    alt = [_oracle_forced(wide_gguf, prompt, toks, fma=False),
+           _oracle_forced(wide_gguf, prompt, toks, block_order=True)]
+    S = max(float(np.abs(a[i] - ref[i]).max()) for a in alt for i in range(len(toks)))
     m = tpthip.Model(ctx, wide_gguf, max_ctx=256, kv_type=tpthip.TYPE_F32)
     try:
         m.decode_path = m.DECODE_PERSISTENT
@@ -153,10 +158,9 @@ def test_wide_persistent_matches_oracle(ctx, wide_gguf):
     finally:
         m.close()
     for i in range(len(toks)):
-        spread = float(np.abs(alt[i] - ref[i]).max())
         dev = float(np.abs(got[i] - ref[i]).max())
-        print(f"step {i}: gpu-oracle {dev:.4f}, oracle fma spread {spread:.4f}")
-        assert dev < 2 * spread + 1e-2, (i, dev, spread)
+        print(f"step {i}: gpu-oracle {dev:.4f}, oracle spread S {S:.4f}")
+        assert dev <= S, (i, dev, S)
 
 
 def test_kv_cache_rows_agree(ctx, tiny_gguf):

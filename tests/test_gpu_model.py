@@ -114,9 +114,12 @@ def test_prefix_prefill_equals_full(tiny_model):
 def test_kv_cache_matches_oracle(tiny_model, tiny_oracle, kv):
     """The K/V rows the prompt and 10 decode steps append, read back with tpt_model_kv_read,
     against the oracle's cache fed the same tokens: layout [kv head][position][head_dim], K after
-    RoPE, V as projected.  f32 cache: within f32 rounding of the GEMV's summation order; fp16
-    cache: the oracle's fp16-rounded values, at most one fp16 ulp apart where an f32 ordering
-    difference moves a value across a rounding boundary."""
+    RoPE, V as projected.  f32 cache: within f32 rounding of the GEMV's summation order.  fp16
+    cache: layer 0 (the same embedding rows on both sides) the oracle's fp16-rounded values, at
+    most one fp16 ulp apart where an f32 ordering difference moves a value across a rounding
+    boundary; layer 1 reads layer 0's output through an fp16 cache and a Q8_K requantization,
+    where such a one-ulp flip grows to a few ulp: relative L2 below 2e-3 (fp16's own rounding is
+    4.9e-4 relative)."""
     n = len(PROMPT)
     first = tiny_model.prefill(PROMPT, 0)
     toks = [first] + tiny_model.decode_greedy(first, n, 10)[:9]  # fed at positions n .. n+9
@@ -130,10 +133,12 @@ def test_kv_cache_matches_oracle(tiny_model, tiny_oracle, kv):
             g, o = g[:, :L], o[:, :L]
             if kv == "f32":
                 assert np.linalg.norm(g - o) / np.linalg.norm(o) < 1e-5, layer
-            else:
+            elif layer == 0:
                 ulp = np.spacing(np.abs(o).astype(np.float16)).astype(np.float32)
                 d = np.abs(g - o)
                 assert np.all(d <= ulp) and np.mean(d > 0) < 0.01, (layer, float((d / ulp).max()))
+            else:
+                assert np.linalg.norm(g - o) / np.linalg.norm(o) < 2e-3, layer
 
 
 def test_context_bounds(tiny_model):
@@ -360,27 +365,20 @@ def mixed_gguf(tmp_path_factory):
 
 
 def test_mixed_q4k_q6k_prefill(ctx, mixed_gguf):
-    """Q6_K layer matrices stay on the batched MFMA prefill (the Q6_K GEMM): the layer holding
-    Q6_K attn_v / ffn_down equals the step path on the same rows (one layer: no rounding flip
-    reaches it), and the 150-token prompt's logits on both prefill paths stay within the
-    oracle's own spread under a change of its dot-product summation order (f32 cache,
-    candle's).  Over 150 positions a Q8_K activation value can round the other way under an f32
-    ordering difference (measured on the step path: 1e-7 from the oracle at 40, 64, 80 and 129
-    tokens, ~1e-2 at 100, 128 and 150), and the random-init model carries such a flip to the
-    logits; so the next token is compared only when the oracle's top-two margin exceeds that
-    bar."""
+    """Q6_K layer matrices stay on the batched MFMA prefill (the Q6_K GEMM):
+    * the layer holding Q6_K attn_v / ffn_down equals the step path on the same rows;
+    * each layer, fed the oracle's own residual rows of a 150-token prompt (teacher-forced, f32
+      cache: candle's), gives the oracle's next rows on both prefill paths within 1e-3
+      relative L2 (only f32 rounding differs on identical inputs).
+    End to end, 150 positions of this random-init model carry an occasional Q8_K rounding flip
+    (under any f32 ordering difference) to the logits, which are therefore only reported."""
     prompt = [int(t) for t in np.random.default_rng(6).integers(0, 1024, 150)]
     om = oracle.Model(mixed_gguf)
     try:
         om.reset(256, kv_f16=False)
-        ref = om.forward(prompt, 0)
-        oracle.set_dot_block_order(True)
-        om.reset(256, kv_f16=False)
-        alt = om.forward(prompt, 0)
+        ref, tr = om.forward_trace(prompt, 0)
     finally:
-        oracle.set_dot_block_order(False)
         om.close()
-    spread = float(np.abs(alt - ref).max())
     m_b = tpthip.Model(ctx, mixed_gguf, max_ctx=256, kv_type=tpthip.TYPE_F32)
     os.environ["TPT_HIP_PREFILL"] = "steps"
     try:
@@ -391,17 +389,17 @@ def test_mixed_q4k_q6k_prefill(ctx, mixed_gguf):
         rows = np.random.default_rng(2).standard_normal((40, m_b.desc["embed"])).astype(np.float32)
         yb = m_b.run_layers(rows, 0, 1, 2, path=0)
         ys = m_s.run_layers(rows, 0, 1, 2, path=1)
-        nb, lb = m_b.prefill(prompt, 0, logits=True)
-        ns, ls = m_s.prefill(prompt, 0, logits=True)
-        print("layer 1 batched vs steps rel-l2", _rel_l2(yb, ys), "| batched vs oracle",
-              np.abs(lb - ref).max(), "| steps vs oracle", np.abs(ls - ref).max(), "| oracle spread", spread)
-        bar = 2 * spread + 1e-3
         assert _rel_l2(yb, ys) < 1e-4
-        assert np.abs(lb - ref).max() < bar
-        assert np.abs(ls - ref).max() < bar
-        top = np.sort(ref)[-2:]
-        if top[1] - top[0] > bar:
-            assert nb == ns == oracle.argmax(ref)
+        errs = []
+        for layer in range(tr.shape[0] - 1):
+            for mm_, path in ((m_b, 0), (m_s, 1)):
+                errs.append(_rel_l2(mm_.run_layers(tr[layer], 0, layer, layer + 1, path=path), tr[layer + 1]))
+        _, lb = m_b.prefill(prompt, 0, logits=True)
+        _, ls = m_s.prefill(prompt, 0, logits=True)
+        print("layer 1 batched vs steps rel-l2", _rel_l2(yb, ys), "| teacher-forced layers rel-l2",
+              [f"{e:.1e}" for e in errs], "| end to end max-abs vs oracle: batched",
+              float(np.abs(lb - ref).max()), "steps", float(np.abs(ls - ref).max()))
+        assert max(errs) < 1e-3, errs
     finally:
         m_b.close()
         m_s.close()
@@ -456,7 +454,7 @@ def oracle_trace_1b(path, kv_mode):
         logits, tr = om.forward_trace(PROMPT_1B, 0, nt)
         tok = oracle.argmax(logits)
         _, tr2 = om.forward_trace([tok], len(PROMPT_1B), nt)
-        kvs = [om.kv(l) for l in range(tr.shape[0] - 1)] if kv_mode == "f32" else None
+        kvs = [om.kv(l) for l in range(tr.shape[0] - 1)]
         om.close()
         _TRACES[kv_mode] = (logits, tr, tok, tr2, kvs)
     return _TRACES[kv_mode]
@@ -633,10 +631,11 @@ def test_1b_teacher_forced_decode(ctx, gguf_1b):
     finally:
         m.close()
     dev = np.abs(got - ref).max(axis=1)
+    rel = np.linalg.norm(got - ref, axis=1) / np.linalg.norm(ref, axis=1)
     margins = np.array([_margin(l) for l in ref])
     close = margins <= S
     print(f"1B teacher-forced, 128 steps: gpu-oracle max-abs logits max {dev.max():.4f} "
-          f"median {np.median(dev):.4f}; oracle spread S {S:.4f} (per step median "
+          f"median {np.median(dev):.4f}, rel-l2 max {rel.max():.4f}; oracle spread S {S:.4f} (per step median "
           f"{np.median(spread):.4f}); logit std {float(ref.std()):.3f}; steps with top-2 margin "
           f"<= S: {int(close.sum())} {np.flatnonzero(close).tolist()}; tokens equal where gated-in: "
           f"{int(sum(g == r for g, r, c in zip(gtok, ref_toks, close) if not c))}/{int((~close).sum())}")
@@ -651,30 +650,28 @@ def test_1b_teacher_forced_decode(ctx, gguf_1b):
 
 @pytest.mark.timeout(900)
 def test_1b_kv_cache_matches_oracle(ctx, gguf_1b, kv):
-    """K/V cache contents after the 128-token prompt, read back with tpt_model_kv_read, against
-    the oracle's cache (the same mode's element type): layout [kv head][position][head_dim] with
-    RoPE applied to K; layer 0 (identical inputs: the embedding rows) to f32 rounding of the
-    GEMV, every layer within the per-layer bar of test_1b_layers_teacher_forced; positions past
-    the prompt untouched (zero)."""
-    om = oracle.Model(gguf_1b)
-    m = tpthip.Model(ctx, gguf_1b, max_ctx=256, kv_type=KV_TYPE[kv])
-    try:
-        om.reset(256, kv_f16=(kv == "f16"))
-        om.forward(PROMPT_1B, 0, min(os.cpu_count() or 1, 16))
-        m.prefill(PROMPT_1B, 0)
-        n = len(PROMPT_1B)
-        worst = []
-        for layer in range(16):
-            gk, gv = m.kv(layer)
-            ok, ov = om.kv(layer)
-            for g, o in ((gk, ok), (gv, ov)):
-                g = g.astype(np.float32)
-                assert g.shape == o.shape == (8, 256, 64)
-                assert not np.any(g[:, n:]), "positions past the prompt were written"
-                e = _rel_l2(g[:, :n], o[:, :n])
-                worst.append(e)
-                assert e < (1e-5 if layer == 0 else (1e-2 if kv == "f32" else 2e-2)), (layer, e)
-        print(kv, "kv rel-l2 per layer (K, V):", " ".join(f"{e:.1e}" for e in worst))
-    finally:
-        m.close()
-        om.close()
+    """K/V cache contents of every layer at the 1B shape, read back with tpt_model_kv_read,
+    against the oracle's cache after the 128-token prompt, each layer fed the oracle's own input
+    rows (teacher-forced, through the batched prefill and through the decode-step kernels), so
+    that each layer's K/V rows come from identical inputs: layout [kv head][position][head_dim]
+    with RoPE applied to K, in the mode's element type, within 2e-4 relative L2 (the f32 order
+    of the RMSNorm and GEMV sums can move a Q8_K activation value by one step, a K/V element by
+    ~5e-4 of its size; fp16's own rounding is 4.9e-4); positions past the prompt untouched."""
+    _, tr, _, _, kvs = oracle_trace_1b(gguf_1b, kv)
+    n = len(PROMPT_1B)
+    worst = {}
+    for path in (0, 1):
+        m = tpthip.Model(ctx, gguf_1b, max_ctx=256, kv_type=KV_TYPE[kv])
+        try:
+            for layer in range(16):
+                m.run_layers(tr[layer], 0, layer, layer + 1, path=path)
+                for g, o, name in zip(m.kv(layer), kvs[layer], "KV"):
+                    assert g.shape == o.shape == (8, 256, 64)
+                    assert not np.any(g[:, n:]), "positions past the prompt were written"
+                    e = _rel_l2(g[:, :n], o[:, :n])
+                    worst[(path, name)] = max(worst.get((path, name), 0.0), e)
+                    assert e < 2e-4, (path, layer, name, e)
+        finally:
+            m.close()
+    print(kv, "kv rel-l2, worst layer:", {f"{'batched' if p == 0 else 'steps'} {n_}": f"{e:.1e}"
+                                          for (p, n_), e in worst.items()})
