@@ -597,9 +597,12 @@ void orc_rope_i(float* x, int n_heads, int hd, const float* c, const float* s) {
 static void attention_impl(const float* q, const float* kc, const float* vc, int nq, int nkv, int hd,
                            int L, int L_stride, float* o, int fma) {
   const float scale = (float)(1.0 / sqrt((double)hd));
-  float* sc = (float*)malloc(sizeof(float) * (size_t)L);
   const int rep = nq / nkv;
+  /* heads are independent (each is its own matmul row in candle): one per thread, every head's
+   * arithmetic in the same order as a serial run */
+#pragma omp parallel for schedule(static) if (L >= 256)
   for (int h = 0; h < nq; h++) {
+    float* sc = (float*)malloc(sizeof(float) * (size_t)L);
     const int g = h / rep;
     const float* qh = q + (size_t)h * hd;
     const float* K = kc + (size_t)g * L_stride * hd;
@@ -624,8 +627,8 @@ static void attention_impl(const float* q, const float* kc, const float* vc, int
       for (int p = 0; p < L; p++) acc = fma ? fmaf(sc[p], V[(size_t)p * hd + d], acc) : acc + sc[p] * V[(size_t)p * hd + d];
       oh[d] = acc;
     }
+    free(sc);
   }
-  free(sc);
 }
 
 void orc_attention(const float* q, const float* kc, const float* vc, int nq, int nkv, int hd,
