@@ -121,6 +121,16 @@ int tpt_attn_decode(tpt_ctx* ctx, const float* q, const void* k_cache, const voi
                     int kv_type, float* o, int nq, int nkv, int hd, int L, int L_stride,
                     int n_chunks);
 
+/* tpt_attn_decode without any device allocation.  No counterpart in the reference: it is for
+ * callers that cannot allocate (code under HIP graph capture, serving loops and harnesses that
+ * must not call hipMalloc).  Same arguments, kernels and results as tpt_attn_decode; the split-K
+ * chunk records live in a fixed 4 MiB device array that each GPU holds until the process ends
+ * (TPT_ERR_UNSUPPORTED when nq * n_chunks * (hd + 2) * 4 bytes exceed it).  Calls that overlap on
+ * one GPU share that array and race. */
+int tpt_attn_decode_noalloc(tpt_ctx* ctx, const float* q, const void* k_cache,
+                            const void* v_cache, int kv_type, float* o, int nq, int nkv, int hd,
+                            int L, int L_stride, int n_chunks);
+
 /* Causal attention of a prompt batch: T query rows q [T][Nq*hd], row t at position L0 + t seeing
  * cache positions [0, L0 + t] (the cache must hold positions < L0 + T); o [T][Nq*hd].  The
  * attention of candle's batched prompt forward (candle_engine.rs:272-273: the whole prompt in one

@@ -80,6 +80,7 @@ EXPORTS = {
     "tpt_rmsnorm": ([P, P, P, P, I32, F32], I32),
     "tpt_rope": ([P, P, I32, I32, I32, P, P], I32),
     "tpt_attn_decode": ([P, P, P, P, I32, P, I32, I32, I32, I32, I32, I32], I32),
+    "tpt_attn_decode_noalloc": ([P, P, P, P, I32, P, I32, I32, I32, I32, I32, I32], I32),
     "tpt_argmax": ([P, P, I64, P], I32),
     "tpt_model_load": ([P, C.c_char_p, I32, I32, PROGRESS_FN, P, P], I32),
     "tpt_model_describe": ([P, P], I32),
