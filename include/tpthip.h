@@ -80,7 +80,11 @@ int tpt_dequant(tpt_ctx* ctx, int type, const void* w, float* y, int64_t n);
 
 /* y[N] = W[N,K] . x[K] with W in GGUF block layout, rows contiguous.  Replaces
  * dequant_and_gemm (wgpu_engine.rs:581-605) + gemm.wgsl:28-70 at M=1, and candle's
- * QMatMul::forward -> k_quants::matmul on the CPU (the parity target). */
+ * QMatMul::forward -> k_quants::matmul on the CPU (the parity target).  type Q4_K, Q5_K, Q6_K,
+ * Q8_0, Q4_0 or F16 (dequant_f16.wgsl, wgpu_engine.rs:543).  act_mode TPT_ACT_Q8: candle's
+ * arithmetic for the type (x quantized to Q8_K / Q8_0 for the quantized types; for F16, which
+ * candle dequantizes and multiplies in f32, x stays f32, K <= 15360); TPT_ACT_F32: the
+ * dequantized weights times f32 x, for every type. */
 int tpt_gemv(tpt_ctx* ctx, int type, const void* w, const float* x, float* y, int K, int N,
              int act_mode);
 

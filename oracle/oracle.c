@@ -498,6 +498,23 @@ int orc_matmul(int type, int64_t m, int64_t k, int64_t n, const float* lhs, cons
     }
     return 0;
   }
+  if (type == ORC_F16) {
+    /* QMatMul::from_arc dequantizes F16 (and F32) weights to an f32 tensor and forward runs
+     * xs.matmul(w.t()): the weights widen exactly and the product is an f32 matmul.  candle's
+     * f32 matmul is the gemm crate; its blocking and summation order are not restated here:
+     * each output is one f32 FMA chain along k (parity unpinned; the GPU's order differs by
+     * f32 rounding only, and tests bound both against an fp64 dot). */
+    const uint16_t* W = (const uint16_t*)w;
+    for (int64_t r = 0; r < m; r++) {
+#pragma omp parallel for num_threads(nthreads) schedule(static)
+      for (int64_t c = 0; c < n; c++) {
+        float s = 0.f;
+        for (int64_t i = 0; i < k; i++) s = fmaf(lhs[r * k + i], orc_fp16_to_f32(W[c * k + i]), s);
+        dst[r * n + c] = s;
+      }
+    }
+    return 0;
+  }
   if (!is_quant_type(type)) return -1;
   const int bs = orc_block_size(type);
   if (k % bs) return -2;

@@ -18,6 +18,7 @@
  *                             both nibbles, the -8 offset)                          PINNED
  *   quantize_q8k / q8_0       hand-computed known answers (tie rule, half-away)     PINNED
  *   vec_dot q4k/q5k/q6k/q8_0/q4_0  fp64 identity over dequantized operands          PINNED
+ *   matmul F16 (dequantize, f32 matmul)  exact widening (every f16 class) + fp64 dot    PINNED
  *   rmsnorm / silu / rope     closed forms (constant vector, 0, pos=0, pair norm)   PINNED
  *   attention                 single position (o=v), uniform scores (o=mean V)      PINNED
  *   argmax                    crafted ties (last index wins), NaN order             PINNED
@@ -65,7 +66,8 @@ int orc_quantize_q8_0(const float* x, int64_t k, orc_blk_q8_0* out);
 /* one output element: candle GgmlType::vec_dot_unopt for the weight type */
 float orc_vec_dot(int type, int64_t k, const void* w_row, const void* act_q);
 
-/* candle k_quants::matmul: dst[M,N] = lhs[M,K] . W[N,K]^T with per-row activation quant.
+/* candle k_quants::matmul: dst[M,N] = lhs[M,K] . W[N,K]^T with per-row activation quant;
+ * F16 / F32 weights: candle's dequantize-then-f32-matmul (no activation quant).
  * nthreads <= 0 uses all cores. */
 int orc_matmul(int type, int64_t m, int64_t k, int64_t n, const float* lhs, const void* w,
                float* dst, int nthreads);

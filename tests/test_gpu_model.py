@@ -405,10 +405,10 @@ def test_mixed_q4k_q6k_prefill(ctx, mixed_gguf):
         m_s.close()
 
 
-@pytest.mark.parametrize("qtype", [tpthip.TYPE_Q5_K, tpthip.TYPE_Q4_0])
+@pytest.mark.parametrize("qtype", [tpthip.TYPE_Q5_K, tpthip.TYPE_Q4_0, tpthip.TYPE_F16])
 def test_other_quant_types_match_oracle(ctx, tmp_path, qtype):
-    """A tiny model whose layer matrices are Q5_K or Q4_0 (token_embd / output Q6_K): the
-    GEMV decode path (these types prefill one position at a time) against the oracle, f32
+    """A tiny model whose layer matrices are Q5_K, Q4_0 or F16 (token_embd / output Q6_K):
+    the GEMV decode path (these types prefill one position at a time) against the oracle, f32
     cache: prompt logits within 1e-3 and the first 16 greedy tokens identical."""
     path = str(tmp_path / f"tiny-{qtype}.gguf")
     synth.write_llama(path, synth.TINY, seed=9, type_matrix=qtype)
@@ -570,14 +570,24 @@ def test_1b_layers_teacher_forced(ctx, gguf_1b, kv):
         assert max(v) < tol, (k, v)
 
 
-def _forced_logits(path, prompt, toks, fma=True, block_order=False, nthreads=16):
-    """Oracle logits at every step of a teacher-forced run (f32 cache, candle's): step 0 after
-    the prompt, step i after feeding toks[i-1]."""
+_FORCED = {}
+
+
+def _forced_logits(path, prompt, toks, fma=True, block_order=False, nthreads=16, kv_f16=False):
+    """Oracle logits at every step of a teacher-forced run (f32 cache, candle's, unless kv_f16):
+    step 0 after the prompt, step i after feeding toks[i-1].  Cached per arguments."""
+    key = (path, tuple(prompt), tuple(toks), fma, block_order, kv_f16)
+    if key not in _FORCED:
+        _FORCED[key] = _forced_logits_run(path, prompt, toks, fma, block_order, nthreads, kv_f16)
+    return _FORCED[key]
+
+
+def _forced_logits_run(path, prompt, toks, fma, block_order, nthreads, kv_f16):
     om = oracle.Model(path)
     try:
         om.set_attn_fma(fma)
         oracle.set_dot_block_order(block_order)
-        om.reset(len(prompt) + len(toks) + 1, kv_f16=False)
+        om.reset(len(prompt) + len(toks) + 1, kv_f16=kv_f16)
         out = [om.forward(prompt, 0, nthreads)]
         for i, t in enumerate(toks[:-1]):
             out.append(om.forward([t], len(prompt) + i, nthreads))
@@ -590,6 +600,35 @@ def _forced_logits(path, prompt, toks, fma=True, block_order=False, nthreads=16)
 def _margin(l):
     top = np.sort(l)[-2:]
     return float(top[1] - top[0])
+
+
+_GREEDY = {}
+
+
+def _greedy_1b(path, nt):
+    """The oracle's (candle's, f32 cache) 128 greedy tokens after the 1B prompt."""
+    if path not in _GREEDY:
+        om = oracle.Model(path)
+        try:
+            _GREEDY[path] = om.greedy(PROMPT_1B, 128, kv_f16=False, nthreads=nt)[0]
+        finally:
+            om.close()
+    return _GREEDY[path]
+
+
+def _gpu_forced(ctx, path, toks, kv_type):
+    """GPU logits and greedy tokens at every step of the teacher-forced 1B run."""
+    m = tpthip.Model(ctx, path, max_ctx=512, kv_type=kv_type)
+    try:
+        nxt, lg = m.prefill(PROMPT_1B, 0, logits=True)
+        got, gtok = [lg], [nxt]
+        for i, t in enumerate(toks[:-1]):
+            nxt, lg = m.decode_step(t, len(PROMPT_1B) + i, logits=True)
+            got.append(lg)
+            gtok.append(nxt)
+    finally:
+        m.close()
+    return np.stack(got), gtok
 
 
 @pytest.mark.timeout(1200)
@@ -607,11 +646,7 @@ def test_1b_teacher_forced_decode(ctx, gguf_1b):
     free-running: the GPU's greedy tokens equal the oracle's up to the first such close step, and
     over at least the first 32 tokens when no close step comes earlier."""
     nt = min(os.cpu_count() or 1, 16)
-    om = oracle.Model(gguf_1b)
-    try:
-        ref_toks, _ = om.greedy(PROMPT_1B, 128, kv_f16=False, nthreads=nt)
-    finally:
-        om.close()
+    ref_toks = _greedy_1b(gguf_1b, nt)
     ref = _forced_logits(gguf_1b, PROMPT_1B, ref_toks, nthreads=nt)
     alt_fma = _forced_logits(gguf_1b, PROMPT_1B, ref_toks, fma=False, nthreads=nt)
     alt_blk = _forced_logits(gguf_1b, PROMPT_1B, ref_toks, block_order=True, nthreads=nt)
@@ -646,6 +681,39 @@ def test_1b_teacher_forced_decode(ctx, gguf_1b):
     assert free[:n_ok] == ref_toks[:n_ok]
     if n_ok >= 32:
         assert free[:32] == ref_toks[:32]
+
+
+@pytest.mark.timeout(1200)
+def test_1b_teacher_forced_decode_fp16_cache(ctx, gguf_1b):
+    """Config 1 with the library's default fp16 KV cache, teacher-forced with candle's greedy
+    tokens (the oracle with candle's f32 cache).  Two bars:
+      * against the oracle run with the same fp16 rounding of the cache: GPU logits within S16,
+        the largest max-abs distance over all steps between that run and the same run in
+        candle's two other plausible orders (no FMA in attention; block-reduced dots);
+      * against candle itself (f32 cache): the fp16 cache is a different arithmetic, and on this
+        model it moves candle's logits by D, the largest distance over all steps between any of
+        the oracle's three fp16-cache runs and candle's f32 run.  The GPU's greedy token equals
+        candle's at every step whose top-two margin exceeds D."""
+    nt = min(os.cpu_count() or 1, 16)
+    ref_toks = _greedy_1b(gguf_1b, nt)
+    ref32 = _forced_logits(gguf_1b, PROMPT_1B, ref_toks, nthreads=nt)
+    ref16 = _forced_logits(gguf_1b, PROMPT_1B, ref_toks, nthreads=nt, kv_f16=True)
+    alt16 = [_forced_logits(gguf_1b, PROMPT_1B, ref_toks, fma=False, nthreads=nt, kv_f16=True),
+             _forced_logits(gguf_1b, PROMPT_1B, ref_toks, block_order=True, nthreads=nt, kv_f16=True)]
+    S16 = max(float(np.abs(a - ref16).max()) for a in alt16)
+    D = max(float(np.abs(c - ref32).max()) for c in [ref16] + alt16)
+    got, gtok = _gpu_forced(ctx, gguf_1b, ref_toks, tpthip.TYPE_F16)
+    dev16 = np.abs(got - ref16).max(axis=1)
+    dev32 = np.abs(got - ref32).max(axis=1)
+    margins = np.array([_margin(l) for l in ref32])
+    decisive = np.flatnonzero(margins > D)
+    print(f"1B fp16 cache, 128 steps: gpu vs oracle(fp16 cache) max {dev16.max():.4f} median "
+          f"{np.median(dev16):.4f}, S16 {S16:.4f}; gpu vs candle(f32 cache) max {dev32.max():.4f} "
+          f"median {np.median(dev32):.4f}, D {D:.4f}; tokens equal at "
+          f"{int(sum(gtok[i] == ref_toks[i] for i in decisive))}/{decisive.size} steps with margin > D")
+    assert dev16.max() <= S16, (dev16.max(), S16)
+    for i in decisive:
+        assert gtok[i] == ref_toks[i], (i, gtok[i], ref_toks[i], margins[i])
 
 
 @pytest.mark.timeout(900)

@@ -13,11 +13,12 @@ import pytest
 
 import oracle
 import tpthip
-from tpthip import synth, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0, TYPE_Q4_0
+from tpthip import synth, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0, TYPE_Q4_0, TYPE_F16
 
 pytestmark = pytest.mark.gpu
 
 QTYPES = [TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0, TYPE_Q4_0]
+GEMV_TYPES = QTYPES + [TYPE_F16]  # F16: candle dequantizes, then an f32 matmul
 
 
 def rel_l2(a, b):
@@ -74,6 +75,15 @@ def test_dequant_hand_blocks_q5k_q4_0(ctx):
     assert list(y[[0, 8, 15, 16, 20, 31]]) == [-4.0, 0.0, 3.5, 3.5, 1.5, -4.0]
 
 
+def test_dequant_f16_every_finite_value(ctx):
+    """Every finite f16 bit pattern (subnormals, both zeros, 65504) widened on the GPU equals
+    numpy's float16 -> float32 conversion bit for bit (the embedding row and F16 GEMV decode)."""
+    bits = np.arange(65536, dtype=np.uint16)
+    bits = bits[(bits & 0x7C00) != 0x7C00]
+    y = ctx.dequant(TYPE_F16, ctx.to_device(bits.view(np.uint8)), bits.size)
+    np.testing.assert_array_equal(y.view(np.uint32), bits.view(np.float16).astype(np.float32).view(np.uint32))
+
+
 GEMV_SHAPES = [(4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)]
 SMALL_SHAPES = [(256, 64), (512, 37), (768, 130), (1024, 300), (2048, 1000), (8192, 520)]
 
@@ -86,7 +96,7 @@ def gemv_case(ctx, qtype, K, N, seed):
 
 
 @pytest.mark.parametrize("K,N", GEMV_SHAPES + SMALL_SHAPES)
-@pytest.mark.parametrize("qtype", QTYPES)
+@pytest.mark.parametrize("qtype", GEMV_TYPES)
 def test_gemv_matches_candle_q8_path(ctx, qtype, K, N):
     w, x, y = gemv_case(ctx, qtype, K, N, seed=K * 7 + N)
     ref = oracle.matmul(qtype, x, w, N)[0]
@@ -96,7 +106,7 @@ def test_gemv_matches_candle_q8_path(ctx, qtype, K, N):
 
 
 @pytest.mark.parametrize("K,N", [(4096, 4096), (14336, 4096), (2048, 1000)])
-@pytest.mark.parametrize("qtype", QTYPES)
+@pytest.mark.parametrize("qtype", GEMV_TYPES)
 def test_gemv_fp32_activations(ctx, qtype, K, N):
     w = synth.random_weights(qtype, N, K, seed=5, name="f32w")
     x = np.random.default_rng(6).standard_normal(K).astype(np.float32)
@@ -105,7 +115,7 @@ def test_gemv_fp32_activations(ctx, qtype, K, N):
     assert rel_l2(y, ref) < 1e-5
 
 
-@pytest.mark.parametrize("qtype", QTYPES)
+@pytest.mark.parametrize("qtype", GEMV_TYPES)
 def test_gemv_rmsnorm_prologue(ctx, qtype):
     K, N, eps = 4096, 2048, 1e-5
     w = synth.random_weights(qtype, N, K, seed=8, name="nw")
@@ -136,8 +146,30 @@ def test_gemv_rejects_bad_shapes(ctx):
         ctx.gemv(TYPE_Q4_K, w, x, 100, 4)
     assert e.value.code == tpthip.ERR_INVALID
     with pytest.raises(tpthip.TptError) as e:
-        ctx.gemv(tpthip.TYPE_F16, w, x, 256, 4)
+        ctx.gemv(tpthip.TYPE_F32, w, x, 256, 4)
     assert e.value.code == tpthip.ERR_UNSUPPORTED
+    with pytest.raises(tpthip.TptError) as e:  # F16 activations in LDS: 4 K bytes
+        ctx.gemv(TYPE_F16, w, x, 16384, 4)
+    assert e.value.code == tpthip.ERR_UNSUPPORTED
+
+
+def test_gemv_f16_exact_extremes(ctx):
+    """F16 rows holding subnormals, +-65504 and zeros against one-hot and power-of-two
+    activations: every product and sum is exact, so the GEMV equals the widened weights
+    (a wrong run interleave, a swapped half or a bf16 reading changes these values)."""
+    K, N = 1024, 64
+    rng = np.random.default_rng(4)
+    specials = np.array([0x0001, 0x03FF, 0x0400, 0x7BFF, 0xFBFF, 0x8000, 0x0000, 0x3C00, 0xBC01],
+                        np.uint16)
+    bits = rng.integers(0, 0x7C00, (N, K)).astype(np.uint16) | (rng.integers(0, 2, (N, K)) << 15).astype(np.uint16)
+    bits[:, :specials.size] = specials
+    wd = ctx.to_device(bits.view(np.uint8).reshape(-1))
+    wf = bits.view(np.float16).astype(np.float32)
+    for j in list(range(specials.size)) + [255, 256, 511, 777, K - 1]:
+        x = np.zeros(K, np.float32)
+        x[j] = 2.0 ** -3
+        y = ctx.gemv(TYPE_F16, wd, ctx.to_device(x), K, N)
+        np.testing.assert_array_equal(y, wf[:, j] * np.float32(2.0 ** -3))
 
 
 def test_rmsnorm_op(ctx):

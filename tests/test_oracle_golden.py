@@ -203,6 +203,30 @@ def test_gemv_f64_linearity():
                                rtol=1e-12, atol=1e-12)
 
 
+def test_f16_matmul_widening_and_fp64():
+    """candle's F16 QMatMul (dequantize to f32, f32 matmul): one-hot activations pick single
+    weights, so every finite f16 value (subnormals, both zeros, +-65504) must come out as
+    numpy's float16 -> float32 widening; random rows stay within f32 rounding of the fp64 dot
+    (a byte swap, a bf16 reading or a dropped term is an O(1) error)."""
+    bits = np.arange(65536, dtype=np.uint16)
+    bits = bits[(bits & 0x7C00) != 0x7C00]
+    k = 256
+    n = bits.size // k
+    w = bits[:n * k].reshape(n, k)
+    for j in (0, 1, 100, 255):
+        x = np.zeros(k, np.float32)
+        x[j] = 1.0
+        y = oracle.matmul(oracle.F16, x, w.view(np.uint8).reshape(-1), n)[0]
+        np.testing.assert_array_equal(y, w[:, j].view(np.float16).astype(np.float32))
+    rng = np.random.default_rng(12)
+    k, n = 4096, 48
+    wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
+    x = rng.standard_normal(k).astype(np.float32)
+    y = oracle.matmul(oracle.F16, x, wf.view(np.uint8).reshape(-1), n)[0]
+    prod = wf.astype(np.float64) * x.astype(np.float64)
+    assert np.all(np.abs(y - prod.sum(1)) <= 1e-5 * np.abs(prod).sum(1))
+
+
 def test_rmsnorm_closed_form():
     n, eps = 4096, 1e-5
     y = oracle.rmsnorm(np.full(n, 2.0, np.float32), np.full(n, 3.0, np.float32), eps)

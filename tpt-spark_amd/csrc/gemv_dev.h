@@ -1,6 +1,6 @@
-// Device code of the fused k-quant dequant-GEMV (see k_gemv.hip for the design): weight-group
-// loads, Q8_K / Q8_0 activation quantization into LDS, integer group dots, and gemv_run, one
-// workgroup's share of a GEMV.
+// Device code of the fused dequant-GEMV (see k_gemv.hip for the design): weight-group loads,
+// Q8_K / Q8_0 activation quantization (or, for F16 weights, the f32 activations) into LDS, group
+// dots, and gemv_run, one workgroup's share of a GEMV.
 #pragma once
 #include "kernels.h"
 
@@ -20,16 +20,23 @@ __device__ __forceinline__ int dpp_i(int v) {
 
 // ----------------------------------------------------------------- per-lane weight groups
 // group g of a row = 64 weights: Q4_K (block g/4, qs bytes 32(g%4)..), Q6_K (block g/4, half
-// (g/2)%2, column half g%2), Q8_0 (blocks 2g, 2g+1)
+// (g/2)%2, column half g%2), Q8_0 (blocks 2g, 2g+1), F16 (the 16-byte runs 4i + g%4, i < 8, of
+// the 512-byte run of 256 weights g/4: the four lanes of a run read 64 contiguous bytes per load)
 template <int WT> struct Raw;
 template <> struct Raw<TPT_TYPE_Q4_K> { uint4 h, a, b; };
 template <> struct Raw<TPT_TYPE_Q6_K> { uint4 qa, qb, qh; uint2 sc; uint32_t d; };
 template <> struct Raw<TPT_TYPE_Q8_0> { uint4 a0, a1, b0, b1; uint32_t d0, d1; };
 template <> struct Raw<TPT_TYPE_Q5_K> { uint4 h, a, b, ha, hb; };
 template <> struct Raw<TPT_TYPE_Q4_0> { uint4 a, b; uint32_t d0, d1; };
+template <> struct Raw<TPT_TYPE_F16> { uint4 v[8]; };
 
-// activation type of a weight type: Q8_0 rows for Q8_0 and Q4_0 weights, Q8_K for the k-quants
-template <int WT> constexpr bool act_q80() { return WT == TPT_TYPE_Q8_0 || WT == TPT_TYPE_Q4_0; }
+// activation form of a weight type: Q8_0 rows for Q8_0 and Q4_0 weights, Q8_K for the k-quants,
+// f32 for F16 weights (candle's QMatMul dequantizes F16 weights to f32 and multiplies in f32)
+enum ActKind { ACT_Q8K = 0, ACT_Q80 = 1, ACT_F32 = 2 };
+template <int WT> constexpr int act_kind() {
+  return WT == TPT_TYPE_F16 ? ACT_F32 : WT == TPT_TYPE_Q8_0 || WT == TPT_TYPE_Q4_0 ? ACT_Q80 : ACT_Q8K;
+}
+template <int WT> constexpr bool act_q80() { return act_kind<WT>() == ACT_Q80; }
 
 template <int WT>
 __device__ __forceinline__ void load_raw(const uint8_t* row, int g, Raw<WT>& r);
@@ -89,31 +96,56 @@ __device__ __forceinline__ void load_raw<TPT_TYPE_Q4_0>(const uint8_t* row, int 
   r.b = ldg_u<uint4>(b0 + 20);
 }
 
+template <>
+__device__ __forceinline__ void load_raw<TPT_TYPE_F16>(const uint8_t* row, int g,
+                                                        Raw<TPT_TYPE_F16>& r) {
+  // rows of K fp16 values, K a multiple of 256: 512-byte runs, 16-byte aligned
+  const uint8_t* b = row + (size_t)(g >> 2) * 512 + 16 * (g & 3);
+#pragma unroll
+  for (int i = 0; i < 8; i++) r.v[i] = *(const uint4*)(b + 64 * i);
+}
+
 // ----------------------------------------------------------------- activation (LDS)
-// LDS layout: qs int8[K] | d float[K/bs] | s16 int[K/16] | scratch float[NW] | rows
+// LDS layout, quantized activations: qs int8[K] | d float[K/bs] | s16 int[K/16] | scratch
+// float[NW] | rows.  f32 activations: xf float[K] | scratch float[NW] | rows.
 struct Lds {
   int* q32;
   float* d;
   int* s16;
+  float* xf;
   float* red;
   float* rows;
 };
 
-__host__ __device__ inline size_t lds_act_bytes(int K, bool q80) {
-  const int nd = q80 ? K / QK8_0 : K / QK_K;
+__host__ __device__ inline size_t lds_act_bytes(int K, int kind) {
+  if (kind == ACT_F32) return 4 * (size_t)K + 4 * NW;
+  const int nd = kind == ACT_Q80 ? K / QK8_0 : K / QK_K;
   return (size_t)K + 4 * nd + 4 * (K / 16) + 4 * NW;
 }
 
-__device__ __forceinline__ Lds lds_layout(char* smem, int K, bool q80) {
+__device__ __forceinline__ Lds lds_layout(char* smem, int K, int kind) {
   Lds l;
   l.q32 = (int*)smem;
-  l.d = (float*)(smem + K);
-  const int nd = q80 ? K / QK8_0 : K / QK_K;
-  l.s16 = (int*)(smem + K + 4 * nd);
-  l.red = (float*)(smem + K + 4 * nd + 4 * (K / 16));
+  l.xf = (float*)smem;
+  if (kind == ACT_F32) {
+    l.d = nullptr;
+    l.s16 = nullptr;
+    l.red = (float*)(smem + 4 * (size_t)K);
+  } else {
+    l.d = (float*)(smem + K);
+    const int nd = kind == ACT_Q80 ? K / QK8_0 : K / QK_K;
+    l.s16 = (int*)(smem + K + 4 * nd);
+    l.red = (float*)(smem + K + 4 * nd + 4 * (K / 16));
+  }
   l.rows = l.red + NW;
   return l;
 }
+
+// f32 activations in LDS: element e of 256-run c sits at word 256c + (e ^ xf_swizzle(c)).  The
+// reader lanes (run, quarter q) of one load take words 32i + 8q + 4h of four consecutive runs;
+// flipping bits 2 and 5 by run puts those 16 four-word groups on distinct banks.  The flip
+// stays inside each lane's own word set, and the prologue's float4 stores stay contiguous.
+__device__ __forceinline__ int xf_swizzle(int c) { return ((c & 1) << 2) | ((c & 2) << 4); }
 
 __device__ __forceinline__ void barrier_lds() {
   // LDS-only barrier: outstanding global loads (the prefetched weights) stay in flight.
@@ -317,12 +349,53 @@ __device__ __forceinline__ void prologue_q80(const GemvArgs& A, const XPre& p, c
   }
 }
 
+// f32 activations (F16 weights): candle's rms_norm output, or x itself, stored unquantized.
+template <int NM = -1>
+__device__ __forceinline__ void prologue_f32(const GemvArgs& A, const XPre& p, const Lds& L) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int nb = A.K / 256;
+  float m = 1.f, rm = 1.f;
+  const bool norm = NM < 0 ? A.prologue == PRO_RMSNORM : NM == 1;
+  if (norm) {
+    m = rms_denominator<false>(A, p, L.red);
+    rm = 1.f / m;
+  }
+#pragma unroll
+  for (int i = 0; i < MAXB; i++) {
+    const int c = wid + i * NW;
+    if (c < nb) {
+      const float4 v = norm ? apply_norm(p.x[i], p.w[i], m, rm) : p.x[i];
+      *(float4*)(L.xf + 256 * c + ((4 * lane) ^ xf_swizzle(c))) = v;
+    }
+  }
+}
+
 // ----------------------------------------------------------------- activation slices
 struct Act {
   int q[16];     // the group's 64 int8 activation values, packed
   float d0, d1;  // Q8_K: d0 = block d;  Q8_0: d of each 32-block
   int s[4];      // Q4_K: s[0], s[1] = sums over each 32;  Q6_K: per-16 sums of the 4 quads
 };
+// F16 weights: the group's 64 f32 activations, x[2i + h] = elements 32i + 8q + 4h .. + 3 of the run
+struct ActF {
+  float4 x[16];
+};
+template <int WT> struct ActOf { using T = Act; };
+template <> struct ActOf<TPT_TYPE_F16> { using T = ActF; };
+
+__device__ __forceinline__ void load_act_f(const Lds& L, int g, ActF& a) {
+  const int c = g >> 2, q = g & 3, sw = xf_swizzle(c);
+  const float* run = L.xf + 256 * c;
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+#pragma unroll
+    for (int h = 0; h < 2; h++) a.x[2 * i + h] = *(const float4*)(run + ((32 * i + 8 * q + 4 * h) ^ sw));
+}
+
+template <int WT>
+__device__ __forceinline__ void load_act(const Lds& L, int g, ActF& a) {
+  load_act_f(L, g, a);
+}
 
 template <int WT>
 __device__ __forceinline__ void load_act(const Lds& L, int g, Act& a) {
@@ -482,6 +555,25 @@ __device__ __forceinline__ float dot_group(const Raw<TPT_TYPE_Q8_0>& r, const Ac
   return ((float)s0 * h2f((uint16_t)r.d0)) * a.d0 + ((float)s1 * h2f((uint16_t)r.d1)) * a.d1;
 }
 
+// F16 x f32 for one group: the dequantized weights (exact) times the f32 activations, f32 FMA
+// in four chains, added as (c0 + c1) + (c2 + c3).  candle's f32 matmul order (the gemm crate's
+// blocking) is not restated.
+__device__ __forceinline__ float dot_group(const Raw<TPT_TYPE_F16>& r, const ActF& a, int) {
+  float c[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const uint32_t w[4] = {r.v[i].x, r.v[i].y, r.v[i].z, r.v[i].w};
+    const float4 x0 = a.x[2 * i], x1 = a.x[2 * i + 1];
+    const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      c[i & 3] = fmaf(h2f((uint16_t)(w[j] & 0xffff)), xs[2 * j], c[i & 3]);
+      c[i & 3] = fmaf(h2f((uint16_t)(w[j] >> 16)), xs[2 * j + 1], c[i & 3]);
+    }
+  }
+  return (c[0] + c[1]) + (c[2] + c[3]);
+}
+
 // K or V cache elements ci, ci+1 (ci even): fp16 pair packed into one 32-bit store, or two f32
 __device__ __forceinline__ void store_kv_pair(void* cache, int kv_type, size_t ci, float a, float b) {
   if (kv_type == TPT_TYPE_F32) {
@@ -537,9 +629,8 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int 
   constexpr int NPART = RowParts<BPP>::N;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int K = A.K, N = A.N;
-  const bool q80 = act_q80<WT>();
   const int nb = K / QK_K;  // super-blocks (256 weights) per row
-  const Lds L = lds_layout(smem, K, q80);
+  const Lds L = lds_layout(smem, K, act_kind<WT>());
   const int RPW = geo.rows_per_wg;
   const int r0 = wg * RPW;
   const int rp = lane / LPR, sb = (lane / 4) % BPP, q = lane & 3;
@@ -589,7 +680,7 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int 
   // 1. activation values next: the loads complete in issue order, so the prologue below only
   //    waits for these, not for the weights issued after them
   XPre xp;
-  preload_x<!act_q80<WT>(), NORM>(A, xp);
+  preload_x<act_kind<WT>() == ACT_Q8K, NORM>(A, xp);
   // every activation load ahead of every weight load, and no prologue arithmetic among them:
   // the prologue then waits only for the former (left alone, the scheduler sinks some
   // activation loads below the weight loads, or hoists the first uses of x above them)
@@ -598,7 +689,8 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int 
   for (int d = 0; d < D; d++) issue(ring[d], d);
   __builtin_amdgcn_sched_barrier(0);
   hook();
-  if constexpr (act_q80<WT>()) prologue_q80<NORM ? 1 : 0>(A, xp, L);
+  if constexpr (act_kind<WT>() == ACT_F32) prologue_f32<NORM ? 1 : 0>(A, xp, L);
+  else if constexpr (act_q80<WT>()) prologue_q80<NORM ? 1 : 0>(A, xp, L);
   else prologue_q8k<NORM ? 1 : 0>(A, xp, L);
   barrier_lds();
 
@@ -621,7 +713,8 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int 
 #pragma unroll
     for (int m = 0; m < NMAT; m++) acc[j][m] = 0.f;
 
-  auto compute = [&](const Raw<WT> (&buf)[RB][NMAT], int s, const Act& act, int g, bool v) {
+  using ActT = typename ActOf<WT>::T;
+  auto compute = [&](const Raw<WT> (&buf)[RB][NMAT], int s, const ActT& act, int g, bool v) {
     const int grp = wr + (s / PP) * WR, p = pa + s % PP;
 #pragma unroll
     for (int j = 0; j < RB; j++)
@@ -654,7 +747,7 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int 
     if constexpr (ONEPASS) {  // this lane's activation slice is the same at every step
       bool v;
       const int g = group_of(pa, &v);
-      Act act;
+      ActT act;
       load_act<WT>(L, g, act);
       for (int s = 0; s < S; s += D) {
 #pragma unroll
@@ -670,7 +763,7 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int 
           if (s + d < S) {
             bool v;
             const int g = group_of(pa + (s + d) % PP, &v);
-            Act act;
+            ActT act;
             load_act<WT>(L, g, act);
             compute(ring[d], s + d, act, g, v);
           }

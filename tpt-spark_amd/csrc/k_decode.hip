@@ -321,7 +321,7 @@ struct AgentX {  // activation float4s written in this launch by other workgroup
 };
 
 __host__ __device__ inline size_t gemv_lds_bytes(int K, int rows) {
-  return (lds_act_bytes(K, false) + 4 * (size_t)rows + 15) & ~(size_t)15;
+  return (lds_act_bytes(K, ACT_Q8K) + 4 * (size_t)rows + 15) & ~(size_t)15;
 }
 
 __device__ __forceinline__ const GLB DecLayer* layer_of(int l) { return cg(s_a.layers) + l; }
@@ -554,7 +554,7 @@ __device__ __noinline__ unsigned ph_qkv(int l, int pos, unsigned e) {
   A.K = H;
   A.prologue = PRO_RMSNORM;
   A.eps = a.eps;
-  const Lds Ls = lds_layout(smem, H, false);
+  const Lds Ls = lds_layout(smem, H, ACT_Q8K);
   if (l == 0) ph.template prologue<true>(A, norm, Ls, LdsX{(const float4*)(smem + a.lds - 4 * (size_t)H)});
   else ph.template prologue<true>(A, norm, Ls, AgentX{rsrc(a.x, 4 * (size_t)H)});
   ph.run(Ls);
@@ -708,7 +708,7 @@ __device__ __noinline__ unsigned ph_wo(int l, unsigned e) {
   GemvArgs A;
   A.K = qd;
   A.prologue = PRO_PLAIN;
-  const Lds Ls = lds_layout(smem, qd, false);
+  const Lds Ls = lds_layout(smem, qd, ACT_Q8K);
   ph.template prologue<false>(A, nullptr, Ls, AgentX{ratt});
   ph.run(Ls);
   const int nr = ph.nrows(), r0 = ph.r0;
@@ -733,7 +733,7 @@ __device__ __noinline__ unsigned ph_gu(int l, unsigned e) {
   A.K = H;
   A.prologue = PRO_RMSNORM;
   A.eps = a.eps;
-  const Lds Ls = lds_layout(smem, H, false);
+  const Lds Ls = lds_layout(smem, H, ACT_Q8K);
   ph.template prologue<true>(A, norm, Ls, AgentX{rx});
   ph.run(Ls);
   const int nr = ph.nrows(), r0 = ph.r0;
@@ -755,7 +755,7 @@ __device__ __noinline__ unsigned ph_dn(int l, unsigned e, bool last) {
   GemvArgs A;
   A.K = F;
   A.prologue = PRO_PLAIN;
-  const Lds Ls = lds_layout(smem, F, false);
+  const Lds Ls = lds_layout(smem, F, ACT_Q8K);
   ph.template prologue<false>(A, nullptr, Ls, AgentX{rh});
   ph.run(Ls);
   const int nr = ph.nrows(), r0 = ph.r0;

@@ -1,4 +1,4 @@
-// Fused k-quant dequant-GEMV for bs=1 decode on gfx950.
+// Fused dequant-GEMV (k-quant, Q8_0 / Q4_0 and F16 weights) for bs=1 decode on gfx950.
 //
 // y[r] = sum_k W[r,k] * x[k], W in GGUF block layout (rows of K/256 super-blocks, uploaded
 // unchanged), x fp32.  Replaces dequant_and_gemm (src-tauri/src/engine/wgpu_engine.rs:581-605:
@@ -10,7 +10,8 @@
 // Work layout (MI355X: 256 CUs, wave64, 160 KB LDS/CU, HBM3E):
 //  * A lane owns a "group" of 64 weights: a quarter of a k-quant super-block (Q4_K: 32 qs bytes
 //    + the block's 16-byte header; Q6_K: one (half, 16-column) slice: 2 x 16 ql bytes, 16 qh
-//    bytes, its 8 scales and d; Q8_0: two 34-byte blocks).  A "pass" covers BPP super-blocks
+//    bytes, its 8 scales and d; Q8_0: two 34-byte blocks; F16: 128 bytes, as eight 16-byte
+//    runs interleaved with the other three lanes of the 256 weights).  A "pass" covers BPP super-blocks
 //    of a row (4 lanes each); when a row has fewer than 16 super-blocks a pass covers
 //    RPP = 16/BPP rows, so every lane of the wave has work.
 //  * A wave runs RB rows in lockstep over a flattened sequence of (row group, pass) steps and
@@ -21,7 +22,9 @@
 //  * Prologue, once per workgroup: x (optionally RMS-normalised) is quantized exactly like
 //    candle's CPU path into LDS -- Q8_K (per 256: signed max-abs value, iscale = -128/max,
 //    round half away from zero, clamp 127, d = 1/iscale, per-16 sums) for k-quant weights,
-//    Q8_0 (per 32: d = amax/127 rounded to f16, q = round(x/d)) for Q8_0 weights.  The x loads
+//    Q8_0 (per 32: d = amax/127 rounded to f16, q = round(x/d)) for Q8_0 weights.  F16 weights
+//    are candle's dequantize-then-f32-matmul: x (or its RMSNorm) stays f32 in LDS and the
+//    group dot is 64 f32 FMAs over the exactly widened weights.  The x loads
 //    are issued first and the first step's weight loads right after, so the prologue runs
 //    under HBM latency.
 //  * Integer dots use v_dot4_i32_i8; each group ends in f32 block scaling (candle's per-block
@@ -173,6 +176,21 @@ __device__ __forceinline__ void dequant64<TPT_TYPE_Q5_K>(const uint8_t* row, int
 }
 
 template <>
+__device__ __forceinline__ void dequant64<TPT_TYPE_F16>(const uint8_t* row, int g, float* y) {
+  const uint4* p = (const uint4*)(row + (size_t)g * 128);  // 64 contiguous weights
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const uint4 v = p[i];
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      y[8 * i + 2 * j] = h2f((uint16_t)(w[j] & 0xffff));
+      y[8 * i + 2 * j + 1] = h2f((uint16_t)(w[j] >> 16));
+    }
+  }
+}
+
+template <>
 __device__ __forceinline__ void dequant64<TPT_TYPE_Q4_0>(const uint8_t* row, int g, float* y) {
   Raw<TPT_TYPE_Q4_0> r;
   load_raw<TPT_TYPE_Q4_0>(row, g, r);
@@ -235,8 +253,11 @@ int launch_cfg(const tpt_ctx* ctx, const GemvArgs& a, int wg_per_cu, hipStream_t
   rpw = (rpw + unit - 1) / unit * unit;
   geo.rows_per_wg = rpw;
   const int grid = (a.N + rpw - 1) / rpw;
-  const size_t lds = lds_act_bytes(a.K, act_q80<WT>()) + 4 * (size_t)KS * rpw * NMAT * RowParts<BPP>::N;
-  if (lds > 65536) return fail(TPT_ERR_UNSUPPORTED, "gemv: too many rows per workgroup for LDS");
+  const size_t lds = lds_act_bytes(a.K, act_kind<WT>()) + 4 * (size_t)KS * rpw * NMAT * RowParts<BPP>::N;
+  if (lds > 65536)
+    return fail(TPT_ERR_UNSUPPORTED, act_kind<WT>() == ACT_F32
+                                         ? "gemv: F16 weights need K * 4 bytes of LDS (K <= 15360)"
+                                         : "gemv: too many rows per workgroup for LDS");
   const bool norm = a.prologue == PRO_RMSNORM, one = geo.P == KS;  // one pass per k-split wave
   if (norm && one) launch_inst<WT, BPP, RB, NMAT, KS, D, true, true>(a, geo, grid, lds, s, ev0, ev1);
   else if (norm) launch_inst<WT, BPP, RB, NMAT, KS, D, true, false>(a, geo, grid, lds, s, ev0, ev1);
@@ -261,6 +282,7 @@ int by_bpp(const tpt_ctx* ctx, const GemvArgs& a, hipStream_t s, hipEvent_t e0, 
 template <int WT, int NMAT>
 int dispatch_shape(const tpt_ctx* ctx, const GemvArgs& a, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
   if constexpr (NMAT == 2) return by_bpp<WT, 2, 1, 2>(ctx, a, s, e0, e1);
+  else if constexpr (WT == TPT_TYPE_F16) return by_bpp<WT, 1, 1, 2>(ctx, a, s, e0, e1);  // 128 B per group
   else {
     if (a.K > 8192) return by_bpp<WT, 1, 2, 2>(ctx, a, s, e0, e1);  // long rows: two rows per step
     return by_bpp<WT, 1, 1, 2>(ctx, a, s, e0, e1);
@@ -285,8 +307,9 @@ int launch_gemv_q8(const tpt_ctx* ctx, int wtype, const GemvArgs& a, hipStream_t
     case TPT_TYPE_Q8_0: return two ? dispatch_shape<TPT_TYPE_Q8_0, 2>(ctx, a, s, ev0, ev1) : dispatch_shape<TPT_TYPE_Q8_0, 1>(ctx, a, s, ev0, ev1);
     case TPT_TYPE_Q5_K: return two ? dispatch_shape<TPT_TYPE_Q5_K, 2>(ctx, a, s, ev0, ev1) : dispatch_shape<TPT_TYPE_Q5_K, 1>(ctx, a, s, ev0, ev1);
     case TPT_TYPE_Q4_0: return two ? dispatch_shape<TPT_TYPE_Q4_0, 2>(ctx, a, s, ev0, ev1) : dispatch_shape<TPT_TYPE_Q4_0, 1>(ctx, a, s, ev0, ev1);
+    case TPT_TYPE_F16: return two ? dispatch_shape<TPT_TYPE_F16, 2>(ctx, a, s, ev0, ev1) : dispatch_shape<TPT_TYPE_F16, 1>(ctx, a, s, ev0, ev1);
   }
-  return fail(TPT_ERR_UNSUPPORTED, "gemv: weight type must be Q4_K, Q5_K, Q6_K, Q8_0 or Q4_0");
+  return fail(TPT_ERR_UNSUPPORTED, "gemv: weight type must be Q4_K, Q5_K, Q6_K, Q8_0, Q4_0 or F16");
 }
 
 int launch_gemv_f32(int wtype, const uint8_t* w, const float* x, float* y, int K, int N,
@@ -300,7 +323,8 @@ int launch_gemv_f32(int wtype, const uint8_t* w, const float* x, float* y, int K
     case TPT_TYPE_Q8_0: hipLaunchKernelGGL(gemv_f32_kernel<TPT_TYPE_Q8_0>, grid, dim3(256), 0, s, w, x, y, K, N, rs); break;
     case TPT_TYPE_Q5_K: hipLaunchKernelGGL(gemv_f32_kernel<TPT_TYPE_Q5_K>, grid, dim3(256), 0, s, w, x, y, K, N, rs); break;
     case TPT_TYPE_Q4_0: hipLaunchKernelGGL(gemv_f32_kernel<TPT_TYPE_Q4_0>, grid, dim3(256), 0, s, w, x, y, K, N, rs); break;
-    default: return fail(TPT_ERR_UNSUPPORTED, "gemv_f32: weight type must be Q4_K, Q5_K, Q6_K, Q8_0 or Q4_0");
+    case TPT_TYPE_F16: hipLaunchKernelGGL(gemv_f32_kernel<TPT_TYPE_F16>, grid, dim3(256), 0, s, w, x, y, K, N, rs); break;
+    default: return fail(TPT_ERR_UNSUPPORTED, "gemv_f32: weight type must be Q4_K, Q5_K, Q6_K, Q8_0, Q4_0 or F16");
   }
   TPT_HIP(hipGetLastError());
   return TPT_OK;

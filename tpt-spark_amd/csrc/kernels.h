@@ -50,7 +50,7 @@ struct GemvArgs {
   unsigned long long* amax = nullptr;  // slot array; slot = state ? amax[state->parity] : amax[0]
 };
 
-// Chooses the lane layout for K and launches.  wtype in {Q4_K, Q6_K, Q8_0}.  ev0/ev1, when
+// Chooses the lane layout for K and launches.  wtype in {Q4_K, Q5_K, Q6_K, Q8_0, Q4_0, F16}.  ev0/ev1, when
 // given, are timestamped by the dispatch itself (hipExtLaunchKernelGGL) around the kernel.
 int launch_gemv_q8(const tpt_ctx* ctx, int wtype, const GemvArgs& a, hipStream_t s,
                    hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);

@@ -24,7 +24,8 @@ using namespace tpt;
 namespace {
 
 bool matrix_type_ok(int t) {
-  return t == TPT_TYPE_Q4_K || t == TPT_TYPE_Q5_K || t == TPT_TYPE_Q6_K || t == TPT_TYPE_Q8_0 || t == TPT_TYPE_Q4_0;
+  return t == TPT_TYPE_Q4_K || t == TPT_TYPE_Q5_K || t == TPT_TYPE_Q6_K || t == TPT_TYPE_Q8_0 || t == TPT_TYPE_Q4_0 ||
+         t == TPT_TYPE_F16;
 }
 
 const char* type_name(int t) {
@@ -144,7 +145,7 @@ static int read_model_meta(const GgufFile& f, tpt_model_desc& desc, ModelTensors
       return rc;
     for (const GgufTensor* m : {t.q, t.k, t.v, t.o, t.g, t.u, t.d})
       if (!matrix_type_ok(m->type))
-        return fail(TPT_ERR_UNSUPPORTED, "tensor " + m->name + " has type " + type_name(m->type) + "; engine-hip reads Q4_K, Q5_K, Q6_K, Q8_0 and Q4_0 matrices");
+        return fail(TPT_ERR_UNSUPPORTED, "tensor " + m->name + " has type " + type_name(m->type) + "; engine-hip reads Q4_K, Q5_K, Q6_K, Q8_0, Q4_0 and F16 matrices");
     if (t.an->type != TPT_TYPE_F32 || t.fn->type != TPT_TYPE_F32) return fail(TPT_ERR_UNSUPPORTED, "norm weights must be F32");
     if (t.g->type != t.u->type)
       return fail(TPT_ERR_UNSUPPORTED, "ffn_gate and ffn_up of different types are not supported yet");
