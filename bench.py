@@ -287,7 +287,7 @@ def main():
     ctx = tp.Context(0)
     log(f"device: {ctx.name}, {ctx.n_cu} CUs")
     if args.leg == "attn":
-        print(json.dumps({"attn_decode": attn_roofline(tp, ctx)}))
+        print(json.dumps({"attn_decode": attn_roofline(tp, ctx), "copy": copy_calibration(ctx)}))
         return
     if args.leg == "gemm":
         print(json.dumps({"prefill_gemm": gemm_roofline(tp, ctx)}))
