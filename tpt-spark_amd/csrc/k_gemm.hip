@@ -274,8 +274,9 @@ __device__ __forceinline__ void stage_store(const Stage<WT>& st, GemmTile& T, Ge
 
 // One K step of MFMAs on tile T (each wave: 64 x 32 as 2 x 1 tiles of 32 x 32).  Q4_K and the
 // fp16 mode: acc += A . B.  Q6_K in GEMM_Q8K mode: the B tile holds the bytes (w0, u) of each
-// weight; two exact chains, hi += A . (u - 64) and lo += A . w0.
-template <int WT, int MODE>
+// weight; two exact chains, hi += A . (u - 64) and lo += A . w0.  FRESH: the chains start here
+// (the first MFMA takes a zero accumulator operand, so no registers are cleared per block).
+template <int WT, int MODE, bool FRESH = false>
 __device__ __forceinline__ void mfma_step(const GemmTile& T, floatx16 (&acc)[2], floatx16 (&lo)[2]) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int wm = wid >> 2, wn = wid & 3;
@@ -297,13 +298,14 @@ __device__ __forceinline__ void mfma_step(const GemmTile& T, floatx16 (&acc)[2],
       const half8 bh = __builtin_bit_cast(half8, h), bl = __builtin_bit_cast(half8, l);
 #pragma unroll
       for (int i = 0; i < 2; i++) {
-        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bh, acc[i], 0, 0, 0);
-        lo[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bl, lo[i], 0, 0, 0);
+        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bh, FRESH && kk == 0 ? floatx16{} : acc[i], 0, 0, 0);
+        lo[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bl, FRESH && kk == 0 ? floatx16{} : lo[i], 0, 0, 0);
       }
     } else {
       const half8 b = *(const half8*)&T.b[sw(32 * wn + lr, kk + lk)];
 #pragma unroll
-      for (int i = 0; i < 2; i++) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b, acc[i], 0, 0, 0);
+      for (int i = 0; i < 2; i++)
+        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b, FRESH && kk == 0 ? floatx16{} : acc[i], 0, 0, 0);
     }
   }
 }
@@ -352,8 +354,6 @@ __device__ __forceinline__ void block_end(const GemmBlock& B, floatx16 (&acc0)[2
         out[i][e] = fmaf(dxs[e], dw * isum, out[i][e]);
       }
     }
-    acc0[i] = floatx16{};
-    acc1[i] = floatx16{};
   }
 }
 
@@ -393,7 +393,7 @@ __global__ void __launch_bounds__(GT, 1) gemm_kernel(const GemmArgs g) {
     // first half
     stage_store<WT, MODE, 1>(st, s.t[1], s.blk[kb & 1]);
     stage_load<WT, MODE, 0>(g, m0, n0, kn, st);
-    if constexpr (MODE == GEMM_Q8K) mfma_step<WT, MODE>(s.t[0], acc0, acc1);
+    if constexpr (MODE == GEMM_Q8K) mfma_step<WT, MODE, true>(s.t[0], acc0, acc1);
     else mfma_step<WT, MODE>(s.t[0], out, out);
     __syncthreads();
     // second half (tile t[1]): stage the next block's first half, fetch its second half
@@ -401,7 +401,7 @@ __global__ void __launch_bounds__(GT, 1) gemm_kernel(const GemmArgs g) {
     stage_load<WT, MODE, 1>(g, m0, n0, kn, st);
     if constexpr (MODE == GEMM_Q8K) {
       if constexpr (Q6) mfma_step<WT, MODE>(s.t[1], acc0, acc1);
-      else mfma_step<WT, MODE>(s.t[1], acc1, acc1);
+      else mfma_step<WT, MODE, true>(s.t[1], acc1, acc1);
     } else {
       mfma_step<WT, MODE>(s.t[1], out, out);
     }
