@@ -88,7 +88,7 @@ int tpt_dequant(tpt_ctx* ctx, int type, const void* w, float* y, int64_t n);
 int tpt_gemv(tpt_ctx* ctx, int type, const void* w, const float* x, float* y, int K, int N,
              int act_mode);
 
-/* Prefill GEMM on MFMA: Y[M,N] = X[M,K] . W[N,K]^T with W in Q4_K or Q6_K rows (type), X fp32
+/* Prefill GEMM on MFMA: Y[M,N] = X[M,K] . W[N,K]^T with W in Q4_K, Q5_K or Q6_K rows (type), X fp32
  * rows (a real Q4_K_M file holds Q6_K attn_v / ffn_down matrices in some layers).
  * act_mode TPT_ACT_Q8: every X row is quantized to Q8_K as candle's QMatMul does and the
  * products are integer-exact (candle's prefill arithmetic); TPT_ACT_F16: X and the dequantized

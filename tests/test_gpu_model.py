@@ -407,9 +407,10 @@ def test_mixed_q4k_q6k_prefill(ctx, mixed_gguf):
 
 @pytest.mark.parametrize("qtype", [tpthip.TYPE_Q5_K, tpthip.TYPE_Q4_0, tpthip.TYPE_F16])
 def test_other_quant_types_match_oracle(ctx, tmp_path, qtype):
-    """A tiny model whose layer matrices are Q5_K, Q4_0 or F16 (token_embd / output Q6_K):
-    the GEMV decode path (these types prefill one position at a time) against the oracle, f32
-    cache: prompt logits within 1e-3 and the first 16 greedy tokens identical."""
+    """A tiny model whose layer matrices are Q5_K, Q4_0 or F16 (token_embd / output Q6_K)
+    against the oracle, f32 cache: prompt logits within 1e-3 and the first 16 greedy tokens
+    identical.  Q5_K prefills through the batched MFMA GEMM (a 150-token prompt is checked
+    too); Q4_0 and F16 prefill one position at a time."""
     path = str(tmp_path / f"tiny-{qtype}.gguf")
     synth.write_llama(path, synth.TINY, seed=9, type_matrix=qtype)
     om = oracle.Model(path)
@@ -428,6 +429,21 @@ def test_other_quant_types_match_oracle(ctx, tmp_path, qtype):
     print(qtype, "logits max-abs vs oracle", float(np.abs(lg - ref).max()))
     assert np.abs(lg - ref).max() < 1e-3
     assert got == want
+    if qtype == tpthip.TYPE_Q5_K:  # a 150-token prompt through the Q5_K MFMA GEMM
+        prompt = [int(t) for t in np.random.default_rng(5).integers(0, 1024, 150)]
+        om = oracle.Model(path)
+        try:
+            om.reset(256, kv_f16=False)
+            ref = om.forward(prompt, 0)
+        finally:
+            om.close()
+        m_b = tpthip.Model(ctx, path, max_ctx=256, kv_type=tpthip.TYPE_F32)
+        try:
+            _, lb = m_b.prefill(prompt, 0, logits=True)
+        finally:
+            m_b.close()
+        print("Q5_K batched 150-token prompt max-abs vs oracle", float(np.abs(lb - ref).max()))
+        assert np.abs(lb - ref).max() < 1e-3
 
 
 @pytest.fixture(scope="module")

@@ -390,7 +390,7 @@ def gemm_case(ctx, M, K, N, seed, bf16=False, qtype=TYPE_Q4_K):
 
 @pytest.mark.parametrize("M,K,N", [(16, 256, 64), (33, 512, 300), (128, 4096, 4096), (200, 2048, 1000),
                                    (130, 14336, 256)])
-@pytest.mark.parametrize("qtype", [TYPE_Q4_K, TYPE_Q6_K])
+@pytest.mark.parametrize("qtype", [TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K])
 def test_gemm_q8k_matches_candle(ctx, M, K, N, qtype):
     """Q8_K mode: candle's prefill arithmetic (each X row quantized to Q8_K, integer dots);
     the integer sums are exact, so only f32 block accumulation order differs."""
@@ -402,7 +402,7 @@ def test_gemm_q8k_matches_candle(ctx, M, K, N, qtype):
         assert rel_l2(y[r], ref[i]) < 1e-5, r
 
 
-@pytest.mark.parametrize("qtype", [TYPE_Q4_K, TYPE_Q6_K])
+@pytest.mark.parametrize("qtype", [TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K])
 def test_gemm_q8k_equals_gemv_rows(ctx, qtype):
     """Batched prefill rows equal the decode GEMV of the same row (same Q8_K arithmetic)."""
     M, K, N = 40, 4096, 512
@@ -441,9 +441,34 @@ def test_gemm_q6k_exact_at_integer_extremes(ctx):
     assert rel_l2(y[5], yv) < 1e-6
 
 
+def q5k_extreme_blocks(n_blocks, seed):
+    """Q5_K blocks (d = 1) with every 5-bit q: half of them with all eight scales and mins 63
+    (integers sc * q up to 1953), half with random packed scales."""
+    rng = np.random.default_rng(seed)
+    b = rng.integers(0, 256, (n_blocks, 176), dtype=np.uint8)  # scales, qh, qs: every value
+    b[: n_blocks // 2, 4:16] = 0xFF  # get_scale_min_k4 reads 63 for every sc and m
+    b[:, 0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    b[:, 2:4] = np.frombuffer(np.float16(0.25).tobytes(), np.uint8)
+    return b.reshape(-1)
+
+
+def test_gemm_q5k_exact_at_integer_extremes(ctx):
+    """Q5_K's integer sums reach 256 * 128 * 1953 (past 2^24) for +-1 activations against
+    scales of 63: the split w = 64 w1 + w0 keeps both chains exact, so the GEMM equals the
+    oracle's integer arithmetic to f32 rounding, and the decode GEMV row for row."""
+    M, K, N = 48, 1024, 64
+    w = q5k_extreme_blocks(N * K // 256, seed=5)
+    x = np.random.default_rng(6).choice(np.array([-1.0, 1.0, 0.5], np.float32), (M, K))
+    y = ctx.gemm(TYPE_Q5_K, ctx.to_device(w), ctx.to_device(x), M, K, N, act=tpthip.ACT_Q8)
+    ref = oracle.matmul(TYPE_Q5_K, x, w, N)
+    assert rel_l2(y, ref) < 1e-6
+    yv = ctx.gemv(TYPE_Q5_K, ctx.to_device(w), ctx.to_device(x[7].copy()), K, N)
+    assert rel_l2(y[7], yv) < 1e-6
+
+
 @pytest.mark.parametrize("M,N,qtype", [(128, 4096, TYPE_Q4_K), (512, 4096, TYPE_Q4_K), (2048, 4096, TYPE_Q4_K),
                                        (128, 14336, TYPE_Q4_K), (512, 14336, TYPE_Q4_K), (2048, 14336, TYPE_Q4_K),
-                                       (512, 4096, TYPE_Q6_K)])
+                                       (512, 4096, TYPE_Q6_K), (512, 4096, TYPE_Q5_K)])
 def test_gemm_f16_config3(ctx, M, N, qtype):
     """fp16 MFMA mode at the prefill shapes (K=4096, bf16 activations): within 1e-3 relative L2
     of the fp64 product of the exactly dequantized weights (checked on a row/column sample)."""
@@ -451,7 +476,7 @@ def test_gemm_f16_config3(ctx, M, N, qtype):
     w, x = gemm_case(ctx, M, K, N, seed=M * 3 + N, bf16=True, qtype=qtype)
     y = ctx.gemm(qtype, ctx.to_device(w), ctx.to_device(x), M, K, N, act=tpthip.ACT_F16)
     nc = min(N, 1024)
-    rb = (K // 256) * (144 if qtype == TYPE_Q4_K else 210)
+    rb = (K // 256) * tpthip.TYPE_SIZE[qtype]
     wdq = oracle.dequant(qtype, w[: nc * rb], nc * K).astype(np.float64).reshape(nc, K)
     rows = np.random.default_rng(1).choice(M, min(M, 64), replace=False)
     ref = x[rows].astype(np.float64) @ wdq.T
@@ -464,4 +489,4 @@ def test_gemm_rejects_bad_shapes(ctx):
     with pytest.raises(tpthip.TptError):
         ctx.gemm(TYPE_Q4_K, w, x, 4, 100, 4, act=tpthip.ACT_Q8)  # K not a multiple of 256
     with pytest.raises(tpthip.TptError):
-        ctx.gemm(TYPE_Q8_0, w, x, 4, 256, 4, act=tpthip.ACT_Q8)  # Q4_K and Q6_K on the MFMA path
+        ctx.gemm(TYPE_Q8_0, w, x, 4, 256, 4, act=tpthip.ACT_Q8)  # Q4_K, Q5_K and Q6_K on the MFMA path

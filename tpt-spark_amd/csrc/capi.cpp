@@ -341,8 +341,8 @@ struct GemmCall {
 };
 int gemm_prepare(tpt_ctx* c, int type, const void* w, const float* x, float* y, int M, int K,
                  int N, int act_mode, GemmCall* call) {
-  if (type != TPT_TYPE_Q4_K && type != TPT_TYPE_Q6_K)
-    return fail(TPT_ERR_UNSUPPORTED, "gemm: weight type must be Q4_K or Q6_K");
+  if (type != TPT_TYPE_Q4_K && type != TPT_TYPE_Q5_K && type != TPT_TYPE_Q6_K)
+    return fail(TPT_ERR_UNSUPPORTED, "gemm: weight type must be Q4_K, Q5_K or Q6_K");
   if (act_mode != TPT_ACT_Q8 && act_mode != TPT_ACT_F16) return fail(TPT_ERR_INVALID, "gemm: act_mode must be TPT_ACT_Q8 or TPT_ACT_F16");
   if (!w || !x || !y || M <= 0 || N <= 0 || K <= 0 || K % 256) return fail(TPT_ERR_INVALID, "gemm: bad arguments");
   GemmArgs& g = call->g;

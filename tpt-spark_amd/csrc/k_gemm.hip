@@ -1,4 +1,4 @@
-// Prefill GEMM on MFMA: Y[M,N] = X[M,K] . W[N,K]^T with W in GGUF Q4_K or Q6_K blocks
+// Prefill GEMM on MFMA: Y[M,N] = X[M,K] . W[N,K]^T with W in GGUF Q4_K, Q5_K or Q6_K blocks
 // (uploaded unchanged), for M >= 16 tokens at once.
 //
 // Replaces the prefill of the reference engines: WgpuEngine runs one whole forward pass per
@@ -18,6 +18,9 @@
 //    split as w = 64 w1 + w0 (w1 in [-64, 64], w0 in [0, 63], both exact in fp16) and two
 //    chains hi += q8 . w1, lo += q8 . w0 run over the whole super-block (|partial| < 2^22,
 //    exact); isum = 64 hi + lo rounds once.
+//    Q5_K weights (vec_dot_q5k_q8k: Q4_K's arithmetic with 5-bit q): w = sc_j * q <= 63 * 31 is
+//    exact in fp16, but 128-element chains could pass 2^24, so w takes Q6_K's split (w = 64 w1 +
+//    w0, two chains over the super-block) and the mins term Q4_K's K=16 MFMA.
 //  * GEMM_F16: the tile is dequantized into LDS as fp16 (Q4_K: d*sc*q - dmin*m, Q6_K:
 //    d*sc*(q - 32), rounded to fp16), the activation is fp16, one fp32 MFMA chain over all of K.
 // Tiling (MI355X: 160 KB LDS, wave64, v_mfma_f32_32x32x16_f16): 512 threads, a 128 x 128 tile
@@ -76,6 +79,8 @@ struct GemmSmem {
 //    (the low nibbles are 16 elements of sub-block 2g, the high nibbles 16 of sub-block 2g + 1).
 //  * Q6_K: quad qt of the half: its 32 ql bytes, the half's 32 qh bytes, the half's 8 int8
 //    scales and d (210-byte blocks are only 2-byte aligned: 16-bit loads).
+//  * Q5_K: Q4_K's header and 16 qs bytes, and the 16 qh bytes of the same l (bits 2g, 2g + 1
+//    are the fifth bits of sub-blocks 2g, 2g + 1); 176-byte blocks stay 16-byte aligned.
 template <int WT> struct Stage;
 template <> struct Stage<TPT_TYPE_Q4_K> {
   u32x4 a[4];
@@ -92,6 +97,19 @@ template <> struct Stage<TPT_TYPE_Q6_K> {
   uint32_t d;
   float dx;
 };
+template <> struct Stage<TPT_TYPE_Q5_K> {
+  u32x4 a[4];
+  u32x4 h;
+  u32x4 q;
+  u32x4 qh;
+  u32x2 a16;
+  float dx;
+};
+
+// Q4_K and Q5_K share the header (d, dmin, packed scales and mins) and the per-16 mins term
+template <int WT> constexpr bool has_mins() { return WT == TPT_TYPE_Q4_K || WT == TPT_TYPE_Q5_K; }
+// Q6_K and Q5_K keep w = 64 w1 + w0 in two exact chains over the whole super-block
+template <int WT> constexpr bool split_w() { return WT == TPT_TYPE_Q6_K || WT == TPT_TYPE_Q5_K; }
 
 __device__ __forceinline__ void get_scale_min(const u32x4& h, int j, int* sc, int* m) {
   // get_scale_min_k4 (ggml/candle): scales bytes s[0..11] are h.y, h.z, h.w
@@ -121,6 +139,13 @@ __device__ __forceinline__ void stage_load(const GemmArgs& g, int m0, int n0, in
     const uint8_t* blk = g.w + (size_t)n * g.w_stride + (size_t)kb * 144;
     st.h = *(const u32x4*)blk;
     st.q = *(const u32x4*)(blk + 16 + 32 * (2 * HB + (qt >> 1)) + 16 * (qt & 1));
+    if constexpr (MODE == GEMM_Q8K && HB == 0)
+      st.a16 = *(const u32x2*)(g.as16 + (size_t)m * (g.K / 16) + kb * 16 + 4 * qt);
+  } else if constexpr (WT == TPT_TYPE_Q5_K) {
+    const uint8_t* blk = g.w + (size_t)n * g.w_stride + (size_t)kb * 176;
+    st.h = *(const u32x4*)blk;
+    st.qh = *(const u32x4*)(blk + 16 + 16 * (qt & 1));
+    st.q = *(const u32x4*)(blk + 48 + 32 * (2 * HB + (qt >> 1)) + 16 * (qt & 1));
     if constexpr (MODE == GEMM_Q8K && HB == 0)
       st.a16 = *(const u32x2*)(g.as16 + (size_t)m * (g.K / 16) + kb * 16 + 4 * qt);
   } else {
@@ -219,6 +244,70 @@ __device__ __forceinline__ void stage_store(const Stage<WT>& st, GemmTile& T, Ge
         *(half8*)&T.b[sw(r, c0 + 32 + 8 * c)] = hi;
       }
     }
+  } else if constexpr (WT == TPT_TYPE_Q5_K) {
+    // as Q4_K (group g = 2 HB + qt / 2, l = 16 (qt % 2) .. + 15), q = nibble + 16 * bit 2g (low)
+    // or 2g + 1 (high) of qh[l]
+    const int g = 2 * HB + (qt >> 1);
+    const int c0 = 64 * (qt >> 1) + 16 * (qt & 1);
+    d = h2f((uint16_t)(st.h.x & 0xffff));
+    dmin = h2f((uint16_t)(st.h.x >> 16));
+    int sc0, m0, sc1, m1;
+    get_scale_min(st.h, 2 * g, &sc0, &m0);
+    get_scale_min(st.h, 2 * g + 1, &sc1, &m1);
+#pragma unroll
+    for (int c = 0; c < 2; c++) {  // 8 consecutive elements (two qs / qh words) per store
+      uint32_t vlo[2], vhi[2];
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const uint32_t x = st.q[2 * c + h], hb = st.qh[2 * c + h];
+        vlo[h] = (x & 0x0F0F0F0Fu) | (((hb >> (2 * g)) & 0x01010101u) << 4);
+        vhi[h] = ((x >> 4) & 0x0F0F0F0Fu) | (((hb >> (2 * g + 1)) & 0x01010101u) << 4);
+      }
+      if constexpr (MODE == GEMM_Q8K) {
+        // w = sc * q <= 1953 as w + 4096 = 64 u + w0 stored as the bytes (w0, u), the layout of
+        // the Q6_K tile (the MFMA operands are then u - 64 and w0)
+        auto split = [&](const uint32_t (&v)[2], int sc) {
+          const short2 s2 = {(short)sc, (short)sc}, c2 = {(short)4096, (short)4096};
+          u32x4 o;
+#pragma unroll
+          for (int h = 0; h < 2; h++) {
+            const uint32_t p01 = __builtin_amdgcn_perm(0u, v[h], 0x0c010c00u);
+            const uint32_t p23 = __builtin_amdgcn_perm(0u, v[h], 0x0c030c02u);
+            const uint32_t w01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(short2, p01) * s2 + c2);
+            const uint32_t w23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(short2, p23) * s2 + c2);
+            o[2 * h] = ((w01 << 2) & 0xFF00FF00u) | (w01 & 0x003F003Fu);
+            o[2 * h + 1] = ((w23 << 2) & 0xFF00FF00u) | (w23 & 0x003F003Fu);
+          }
+          return o;
+        };
+        *(u32x4*)&T.b[sw(r, c0 + 8 * c)] = split(vlo, sc0);
+        *(u32x4*)&T.b[sw(r, c0 + 32 + 8 * c)] = split(vhi, sc1);
+      } else {
+        const float d1 = d * (float)sc0, mm1 = dmin * (float)m0;
+        const float d2 = d * (float)sc1, mm2 = dmin * (float)m1;
+        half8 lo, hi;
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+          lo[t] = (_Float16)(d1 * (float)((vlo[t / 4] >> (8 * (t % 4))) & 0xff) - mm1);
+          hi[t] = (_Float16)(d2 * (float)((vhi[t / 4] >> (8 * (t % 4))) & 0xff) - mm2);
+        }
+        *(half8*)&T.b[sw(r, c0 + 8 * c)] = lo;
+        *(half8*)&T.b[sw(r, c0 + 32 + 8 * c)] = hi;
+      }
+    }
+    if constexpr (MODE == GEMM_Q8K) {
+      const half2 mm0 = {(_Float16)m0, (_Float16)m0}, mm1 = {(_Float16)m1, (_Float16)m1};
+      *(u32x2*)&B.b16[r][4 * g] = u32x2{__builtin_bit_cast(uint32_t, mm0), __builtin_bit_cast(uint32_t, mm1)};
+      if constexpr (HB == 0) {
+        u32x2 v;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+          const half2 p = {(_Float16)(int16_t)(st.a16[j] & 0xffff), (_Float16)(int16_t)(st.a16[j] >> 16)};
+          v[j] = __builtin_bit_cast(uint32_t, p);
+        }
+        *(u32x2*)&B.a16[r][4 * qt] = v;
+      }
+    }
   } else {
     // Q6_K half HB of a super-block, elements 32 Q + l of the half (quad Q, l < 32):
     //   q = ((ql[32 (Q & 1) + l] >> 4 (Q >= 2)) & 15) | ((qh[l] >> 2 Q) & 3) << 4,
@@ -286,7 +375,7 @@ __device__ __forceinline__ void mfma_step(const GemmTile& T, floatx16 (&acc)[2],
     half8 a[2];
 #pragma unroll
     for (int i = 0; i < 2; i++) a[i] = *(const half8*)&T.a[sw(64 * wm + 32 * i + lr, kk + lk)];
-    if constexpr (WT == TPT_TYPE_Q6_K && MODE == GEMM_Q8K) {
+    if constexpr (split_w<WT>() && MODE == GEMM_Q8K) {
       const u32x4 raw = *(const u32x4*)&T.b[sw(32 * wn + lr, kk + lk)];
       const half2 k1088 = {(_Float16)1088.f, (_Float16)1088.f}, k1024 = {(_Float16)1024.f, (_Float16)1024.f};
       u32x4 h, l;
@@ -325,7 +414,7 @@ __device__ __forceinline__ void block_end(const GemmBlock& B, floatx16 (&acc0)[2
   const float dw = B.dw[col];
   half8 b;
   float dm = 0.f;
-  if constexpr (WT == TPT_TYPE_Q4_K) {
+  if constexpr (has_mins<WT>()) {
     b = *(const half8*)&B.b16[col][lk];
     dm = B.dm[col];
   }
@@ -338,12 +427,13 @@ __device__ __forceinline__ void block_end(const GemmBlock& B, floatx16 (&acc0)[2
       const float4 v = *(const float4*)&B.dx[64 * wm + 32 * i + q * 8 + (lane >> 5) * 4];
       dxs[4 * q] = v.x; dxs[4 * q + 1] = v.y; dxs[4 * q + 2] = v.z; dxs[4 * q + 3] = v.w;
     }
-    if constexpr (WT == TPT_TYPE_Q4_K) {
+    if constexpr (has_mins<WT>()) {
       const half8 a = *(const half8*)&B.a16[64 * wm + 32 * i + lr][lk];
       const floatx16 accm = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, floatx16{}, 0, 0, 0);
 #pragma unroll
       for (int e = 0; e < 16; e++) {
-        const float isum = acc0[i][e] + acc1[i][e];
+        // Q4_K: the two exact half chains; Q5_K: 64 hi + lo
+        const float isum = split_w<WT>() ? fmaf(64.f, acc0[i][e], acc1[i][e]) : acc0[i][e] + acc1[i][e];
         const float t = fmaf(dw, isum, -(dm * accm[e]));
         out[i][e] = fmaf(dxs[e], t, out[i][e]);
       }
@@ -369,7 +459,7 @@ __global__ void __launch_bounds__(GT, 1) gemm_kernel(const GemmArgs g) {
   const int lr = lane & 31;
   // chains: Q4_K q8k acc0 / acc1 = the two halves of a super-block; Q6_K q8k acc0 / acc1 =
   // hi / lo over the whole super-block; fp16 mode: out directly
-  constexpr bool Q6 = WT == TPT_TYPE_Q6_K;
+  constexpr bool Q6 = split_w<WT>();  // Q6_K, Q5_K: hi / lo chains over the super-block
 
   floatx16 out[2], acc0[2], acc1[2];
 #pragma unroll
@@ -519,16 +609,17 @@ int launch_gemm(const GemmArgs& g, hipStream_t s) { return launch_gemm_timed(g, 
 
 int launch_gemm_timed(const GemmArgs& g, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.K % 256) return fail(TPT_ERR_INVALID, "gemm: K must be a positive multiple of 256, M and N positive");
-  if (g.wtype != TPT_TYPE_Q4_K && g.wtype != TPT_TYPE_Q6_K) return fail(TPT_ERR_UNSUPPORTED, "gemm: weight type must be Q4_K or Q6_K");
+  if (g.wtype != TPT_TYPE_Q4_K && g.wtype != TPT_TYPE_Q5_K && g.wtype != TPT_TYPE_Q6_K)
+    return fail(TPT_ERR_UNSUPPORTED, "gemm: weight type must be Q4_K, Q5_K or Q6_K");
   if (g.mode != GEMM_Q8K && g.mode != GEMM_F16) return fail(TPT_ERR_INVALID, "gemm: bad activation mode");
   if (!g.w || !g.y) return fail(TPT_ERR_INVALID, "gemm: null weight/output pointer");
   if (!g.af) return fail(TPT_ERR_INVALID, "gemm: null activation rows");
-  if (g.mode == GEMM_Q8K && (!g.ad || (g.wtype == TPT_TYPE_Q4_K && !g.as16)))
-    return fail(TPT_ERR_INVALID, "gemm: Q8_K mode needs block scales (and per-16 sums for Q4_K)");
-  if (g.w_stride < (size_t)(g.K / 256) * (g.wtype == TPT_TYPE_Q4_K ? 144 : 210))
+  if (g.mode == GEMM_Q8K && (!g.ad || (g.wtype != TPT_TYPE_Q6_K && !g.as16)))
+    return fail(TPT_ERR_INVALID, "gemm: Q8_K mode needs block scales (and per-16 sums for Q4_K and Q5_K)");
+  if (g.w_stride < (size_t)(g.K / 256) * type_bytes(g.wtype))
     return fail(TPT_ERR_INVALID, "gemm: weight row stride shorter than a row");
-  if (g.wtype == TPT_TYPE_Q4_K && ((g.w_stride % 16) || ((uintptr_t)g.w % 16)))
-    return fail(TPT_ERR_INVALID, "gemm: Q4_K weight rows must be 16-byte aligned");
+  if (g.wtype != TPT_TYPE_Q6_K && ((g.w_stride % 16) || ((uintptr_t)g.w % 16)))
+    return fail(TPT_ERR_INVALID, "gemm: Q4_K and Q5_K weight rows must be 16-byte aligned");
   if (g.wtype == TPT_TYPE_Q6_K && ((g.w_stride % 2) || ((uintptr_t)g.w % 2)))
     return fail(TPT_ERR_INVALID, "gemm: Q6_K weight rows must be 2-byte aligned");
   int ns = gemm_splits(g.M, g.N, g.K);
@@ -538,6 +629,9 @@ int launch_gemm_timed(const GemmArgs& g, hipStream_t s, hipEvent_t ev0, hipEvent
   if (g.wtype == TPT_TYPE_Q4_K) {
     if (g.mode == GEMM_Q8K) hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q4_K, GEMM_Q8K>), grid, dim3(GT), 0, s, ev0, e1, 0, g);
     else hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q4_K, GEMM_F16>), grid, dim3(GT), 0, s, ev0, e1, 0, g);
+  } else if (g.wtype == TPT_TYPE_Q5_K) {
+    if (g.mode == GEMM_Q8K) hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q5_K, GEMM_Q8K>), grid, dim3(GT), 0, s, ev0, e1, 0, g);
+    else hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q5_K, GEMM_F16>), grid, dim3(GT), 0, s, ev0, e1, 0, g);
   } else {
     if (g.mode == GEMM_Q8K) hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q6_K, GEMM_Q8K>), grid, dim3(GT), 0, s, ev0, e1, 0, g);
     else hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q6_K, GEMM_F16>), grid, dim3(GT), 0, s, ev0, e1, 0, g);

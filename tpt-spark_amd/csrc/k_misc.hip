@@ -1,5 +1,7 @@
 // Small kernels of the decode path: bit-exact dequantization, the decode-step prologue
 // (token pick + embedding row), RMSNorm, RoPE and argmax as standalone ops.
+#include <cstddef>
+
 #include "kernels.h"
 
 namespace tpt {
@@ -15,6 +17,13 @@ __global__ void dequant_kernel(int type, const uint8_t* __restrict__ w, float* _
 // Decode-step prologue (one workgroup): the token of this position (prompt, host override or
 // the previous step's argmax), then its embedding row: the row's bytes are staged in LDS with
 // independent 2-byte loads (every GGUF row length here is even) and dequantized from there.
+// The whole step state is read in one round trip (three 16-byte loads, both argmax slots), so
+// a decode step waits for two dependent loads (state, row) before the row is in LDS.
+static_assert(offsetof(StepState, next_pos) == 4 && offsetof(StepState, parity) == 8 &&
+                  offsetof(StepState, use_override) == 12 && offsetof(StepState, tok_override) == 16 &&
+                  offsetof(StepState, prompt_len) == 20 && offsetof(StepState, amax) == 32 &&
+                  sizeof(StepState) == 48,
+              "step_begin_kernel reads StepState as three 16-byte words");
 __global__ void __launch_bounds__(256) step_begin_kernel(StepState* st, const uint32_t* prompt,
                                                          int embd_type, const uint8_t* embd,
                                                          size_t embd_row_bytes, int H, int vocab,
@@ -23,11 +32,14 @@ __global__ void __launch_bounds__(256) step_begin_kernel(StepState* st, const ui
   __shared__ uint32_t s_tok;
   __shared__ int s_pos;
   if (threadIdx.x == 0) {
-    const int pos = st->next_pos;
+    const uint4* sw = (const uint4*)st;  // 256-byte aligned in the runtime buffer
+    const uint4 w0 = sw[0], w1 = sw[1], w2 = sw[2];
+    const int pos = (int)w0.y, parity = (int)w0.z, use_override = (int)w0.w;
+    const int prompt_len = (int)w1.y;
     uint32_t tok;
-    if (pos < st->prompt_len) tok = prompt[pos];
-    else if (st->use_override) tok = st->tok_override;
-    else tok = (uint32_t)(st->amax[st->parity] & 0xffffffffull);
+    if (pos < prompt_len) tok = prompt[pos];
+    else if (use_override) tok = w1.x;
+    else tok = parity ? w2.z : w2.x;  // low 32 bits of amax[parity]: the index
     if (tok >= (uint32_t)vocab) tok = (uint32_t)(vocab - 1);  // never index past the table
     s_tok = tok;
     s_pos = pos;

@@ -57,11 +57,11 @@ int launch_gemv_q8(const tpt_ctx* ctx, int wtype, const GemvArgs& a, hipStream_t
 int launch_gemv_f32(int wtype, const uint8_t* w, const float* x, float* y, int K, int N,
                     hipStream_t s);
 
-// ---- prefill GEMM (k_gemm.hip): Y[M,N] = X[M,K] . W[N,K]^T, W in Q4_K or Q6_K blocks
+// ---- prefill GEMM (k_gemm.hip): Y[M,N] = X[M,K] . W[N,K]^T, W in Q4_K, Q5_K or Q6_K blocks
 enum GemmMode { GEMM_Q8K = 0, GEMM_F16 = 1 };
 struct GemmArgs {
   int M = 0, N = 0, K = 0, mode = GEMM_Q8K;
-  int wtype = TPT_TYPE_Q4_K;         // weight blocks: TPT_TYPE_Q4_K or TPT_TYPE_Q6_K
+  int wtype = TPT_TYPE_Q4_K;         // weight blocks: TPT_TYPE_Q4_K, TPT_TYPE_Q5_K or TPT_TYPE_Q6_K
   const uint8_t* w = nullptr;
   size_t w_stride = 0;               // bytes per weight row
   const uint16_t* af = nullptr;      // [M][K] fp16 bits (GEMM_Q8K: the Q8_K int8 values, exact)

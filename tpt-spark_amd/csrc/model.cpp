@@ -331,7 +331,7 @@ int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_t
   batched_prefill = true;
   for (const Layer& L : layers)
     for (int t : {L.tq, L.tk, L.tv, L.to, L.tg, L.tu, L.td})
-      if (t != TPT_TYPE_Q4_K && t != TPT_TYPE_Q6_K) batched_prefill = false;
+      if (t != TPT_TYPE_Q4_K && t != TPT_TYPE_Q5_K && t != TPT_TYPE_Q6_K) batched_prefill = false;
   const char* ev_pf = getenv("TPT_HIP_PREFILL");
   if (ev_pf && strcmp(ev_pf, "steps") == 0) batched_prefill = false;
   const char* ev_att = getenv("TPT_HIP_CAUSAL_ATTN");
@@ -781,7 +781,7 @@ int tpt_model::run_layers(const float* x_in, int n, int pos0, int l0, int l1, in
   if (n <= 0 || pos0 < 0 || pos0 + n > desc.max_ctx || l0 < 0 || l1 > desc.n_layers || l0 > l1 ||
       (path != 0 && path != 1))
     return fail(TPT_ERR_INVALID, "run_layers: bad range or path");
-  if (path == 0 && !batched_prefill) return fail(TPT_ERR_UNSUPPORTED, "run_layers: batched path needs Q4_K layer matrices");
+  if (path == 0 && !batched_prefill) return fail(TPT_ERR_UNSUPPORTED, "run_layers: batched path needs Q4_K, Q5_K or Q6_K layer matrices");
   int rc;
   if (path == 0) {
     for (int c0 = 0; c0 < n; c0 += kPrefillT) {
