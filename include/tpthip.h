@@ -88,12 +88,15 @@ int tpt_dequant(tpt_ctx* ctx, int type, const void* w, float* y, int64_t n);
 int tpt_gemv(tpt_ctx* ctx, int type, const void* w, const float* x, float* y, int K, int N,
              int act_mode);
 
-/* Prefill GEMM on MFMA: Y[M,N] = X[M,K] . W[N,K]^T with W in Q4_K, Q5_K or Q6_K rows (type), X fp32
- * rows (a real Q4_K_M file holds Q6_K attn_v / ffn_down matrices in some layers).
- * act_mode TPT_ACT_Q8: every X row is quantized to Q8_K as candle's QMatMul does and the
- * products are integer-exact (candle's prefill arithmetic); TPT_ACT_F16: X and the dequantized
- * W in fp16 on the matrix cores, fp32 accumulate.  Replaces the per-position prefill of
- * gpu_infer (wgpu_engine.rs:254-261) and candle's batched QMatMul (candle_engine.rs:272-273). */
+/* Prefill GEMM on MFMA: Y[M,N] = X[M,K] . W[N,K]^T with W in Q4_K, Q5_K, Q6_K, Q8_0, Q4_0 or
+ * F16 rows (type), X fp32 rows (a real Q4_K_M file holds Q6_K attn_v / ffn_down matrices in
+ * some layers).  act_mode TPT_ACT_Q8 is candle's prefill arithmetic for the type: every X row
+ * quantized to Q8_K (k-quants) or Q8_0 (Q8_0, Q4_0 weights) as candle's QMatMul does, with
+ * integer-exact products; for F16 weights, which candle multiplies in f32, X split into fp16
+ * rounding plus remainder (two passes, X carried to 2^-22 relative; |X| < 65504).
+ * TPT_ACT_F16 (k-quants and F16): X and the dequantized W in fp16 on the matrix cores, fp32
+ * accumulate.  Replaces the per-position prefill of gpu_infer (wgpu_engine.rs:254-261) and
+ * candle's batched QMatMul (candle_engine.rs:272-273). */
 int tpt_gemm(tpt_ctx* ctx, int type, const void* w, const float* x, float* y, int M, int K, int N,
              int act_mode);
 

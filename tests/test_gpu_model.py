@@ -409,8 +409,13 @@ def test_mixed_q4k_q6k_prefill(ctx, mixed_gguf):
 def test_other_quant_types_match_oracle(ctx, tmp_path, qtype):
     """A tiny model whose layer matrices are Q5_K, Q4_0 or F16 (token_embd / output Q6_K)
     against the oracle, f32 cache: prompt logits within 1e-3 and the first 16 greedy tokens
-    identical.  Q5_K prefills through the batched MFMA GEMM (a 150-token prompt is checked
-    too); Q4_0 and F16 prefill one position at a time."""
+    identical.  Then a 150-token prompt through the batched MFMA prefill of the type (Q8_K
+    activations for Q5_K, Q8_0 for Q4_0, the f32 split for F16), each layer fed the oracle's
+    own input rows: for F16, where no activation is quantized, within 1e-5 relative L2; for the
+    quantized types within 1e-2, the bar of the 1B teacher-forced layers -- over 150 positions
+    an activation that sits on a rounding boundary of its Q8 quantization can round the other
+    way under a different f32 summation order of the RMSNorm (4.6e-3 measured at layer 0 of
+    the Q4_0 model, on the batched and the step-by-step path alike)."""
     path = str(tmp_path / f"tiny-{qtype}.gguf")
     synth.write_llama(path, synth.TINY, seed=9, type_matrix=qtype)
     om = oracle.Model(path)
@@ -429,21 +434,20 @@ def test_other_quant_types_match_oracle(ctx, tmp_path, qtype):
     print(qtype, "logits max-abs vs oracle", float(np.abs(lg - ref).max()))
     assert np.abs(lg - ref).max() < 1e-3
     assert got == want
-    if qtype == tpthip.TYPE_Q5_K:  # a 150-token prompt through the Q5_K MFMA GEMM
-        prompt = [int(t) for t in np.random.default_rng(5).integers(0, 1024, 150)]
-        om = oracle.Model(path)
-        try:
-            om.reset(256, kv_f16=False)
-            ref = om.forward(prompt, 0)
-        finally:
-            om.close()
-        m_b = tpthip.Model(ctx, path, max_ctx=256, kv_type=tpthip.TYPE_F32)
-        try:
-            _, lb = m_b.prefill(prompt, 0, logits=True)
-        finally:
-            m_b.close()
-        print("Q5_K batched 150-token prompt max-abs vs oracle", float(np.abs(lb - ref).max()))
-        assert np.abs(lb - ref).max() < 1e-3
+    prompt = [int(t) for t in np.random.default_rng(5).integers(0, 1024, 150)]
+    om = oracle.Model(path)
+    try:
+        om.reset(256, kv_f16=False)
+        _, tr = om.forward_trace(prompt, 0)
+    finally:
+        om.close()
+    m_b = tpthip.Model(ctx, path, max_ctx=256, kv_type=tpthip.TYPE_F32)
+    try:
+        errs = [_rel_l2(m_b.run_layers(tr[l], 0, l, l + 1, path=0), tr[l + 1]) for l in range(tr.shape[0] - 1)]
+    finally:
+        m_b.close()
+    print(qtype, "batched 150-token prompt, teacher-forced layers rel-l2", [f"{e:.1e}" for e in errs])
+    assert max(errs) < (1e-5 if qtype == tpthip.TYPE_F16 else 1e-2)
 
 
 @pytest.fixture(scope="module")

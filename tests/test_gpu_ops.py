@@ -390,10 +390,11 @@ def gemm_case(ctx, M, K, N, seed, bf16=False, qtype=TYPE_Q4_K):
 
 @pytest.mark.parametrize("M,K,N", [(16, 256, 64), (33, 512, 300), (128, 4096, 4096), (200, 2048, 1000),
                                    (130, 14336, 256)])
-@pytest.mark.parametrize("qtype", [TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K])
+@pytest.mark.parametrize("qtype", GEMV_TYPES)
 def test_gemm_q8k_matches_candle(ctx, M, K, N, qtype):
-    """Q8_K mode: candle's prefill arithmetic (each X row quantized to Q8_K, integer dots);
-    the integer sums are exact, so only f32 block accumulation order differs."""
+    """TPT_ACT_Q8: candle's prefill arithmetic for the weight type (each X row quantized to
+    Q8_K for the k-quants, to Q8_0 for Q8_0 / Q4_0 weights, integer dots; for F16 weights an f32
+    product); the integer sums are exact, so only f32 block accumulation order differs."""
     w, x = gemm_case(ctx, M, K, N, seed=M + K + N, qtype=qtype)
     y = ctx.gemm(qtype, ctx.to_device(w), ctx.to_device(x), M, K, N, act=tpthip.ACT_Q8)
     rows = np.arange(M) if M * N <= 200 * 1000 else np.random.default_rng(0).choice(M, 24, replace=False)
@@ -402,7 +403,7 @@ def test_gemm_q8k_matches_candle(ctx, M, K, N, qtype):
         assert rel_l2(y[r], ref[i]) < 1e-5, r
 
 
-@pytest.mark.parametrize("qtype", [TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K])
+@pytest.mark.parametrize("qtype", GEMV_TYPES)
 def test_gemm_q8k_equals_gemv_rows(ctx, qtype):
     """Batched prefill rows equal the decode GEMV of the same row (same Q8_K arithmetic)."""
     M, K, N = 40, 4096, 512
@@ -489,4 +490,6 @@ def test_gemm_rejects_bad_shapes(ctx):
     with pytest.raises(tpthip.TptError):
         ctx.gemm(TYPE_Q4_K, w, x, 4, 100, 4, act=tpthip.ACT_Q8)  # K not a multiple of 256
     with pytest.raises(tpthip.TptError):
-        ctx.gemm(TYPE_Q8_0, w, x, 4, 256, 4, act=tpthip.ACT_Q8)  # Q4_K, Q5_K and Q6_K on the MFMA path
+        ctx.gemm(TYPE_Q8_0, w, x, 4, 256, 4, act=tpthip.ACT_F16)  # Q8_0 and Q4_0: Q8_0 activations only
+    with pytest.raises(tpthip.TptError):
+        ctx.gemm(tpthip.TYPE_F32, w, x, 4, 256, 4, act=tpthip.ACT_Q8)

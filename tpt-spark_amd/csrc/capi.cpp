@@ -334,20 +334,38 @@ int tpt_argmax(tpt_ctx* c, const float* logits, int64_t n, uint32_t* out_host) {
 }
 
 namespace {
-// Device scratch for one tpt_gemm / tpt_bench_gemm call: the prepared activation rows.
+// Device scratch for one tpt_gemm / tpt_bench_gemm call: the prepared activation rows.  F16
+// weights in TPT_ACT_Q8 mode (candle's f32 product) run two passes: on the fp16 remainder rows
+// (lo), then on the fp16 rows with the first pass's output as the residual.
 struct GemmCall {
   GemmArgs g;
+  const uint16_t* lo = nullptr;
   void* scratch = nullptr;
 };
+int gemm_run(const GemmCall& call, hipStream_t s, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr) {
+  if (!call.lo) return launch_gemm_timed(call.g, s, ev0, ev1);
+  GemmArgs g = call.g;
+  g.af = call.lo;
+  int rc = launch_gemm_timed(g, s, ev0, nullptr);
+  if (rc) return rc;
+  g.af = call.g.af;
+  g.resid = g.y;
+  g.ldr = g.ldy;
+  return launch_gemm_timed(g, s, nullptr, ev1);
+}
 int gemm_prepare(tpt_ctx* c, int type, const void* w, const float* x, float* y, int M, int K,
                  int N, int act_mode, GemmCall* call) {
-  if (type != TPT_TYPE_Q4_K && type != TPT_TYPE_Q5_K && type != TPT_TYPE_Q6_K)
-    return fail(TPT_ERR_UNSUPPORTED, "gemm: weight type must be Q4_K, Q5_K or Q6_K");
+  const bool kq = type == TPT_TYPE_Q4_K || type == TPT_TYPE_Q5_K || type == TPT_TYPE_Q6_K;
+  const bool q80 = type == TPT_TYPE_Q8_0 || type == TPT_TYPE_Q4_0;
+  if (!kq && !q80 && type != TPT_TYPE_F16)
+    return fail(TPT_ERR_UNSUPPORTED, "gemm: weight type must be Q4_K, Q5_K, Q6_K, Q8_0, Q4_0 or F16");
   if (act_mode != TPT_ACT_Q8 && act_mode != TPT_ACT_F16) return fail(TPT_ERR_INVALID, "gemm: act_mode must be TPT_ACT_Q8 or TPT_ACT_F16");
+  if (q80 && act_mode != TPT_ACT_Q8) return fail(TPT_ERR_UNSUPPORTED, "gemm: Q8_0 and Q4_0 weights take TPT_ACT_Q8");
   if (!w || !x || !y || M <= 0 || N <= 0 || K <= 0 || K % 256) return fail(TPT_ERR_INVALID, "gemm: bad arguments");
   GemmArgs& g = call->g;
   g.M = M; g.N = N; g.K = K;
-  g.mode = act_mode == TPT_ACT_Q8 ? GEMM_Q8K : GEMM_F16;
+  g.mode = act_mode == TPT_ACT_F16 || type == TPT_TYPE_F16 ? GEMM_F16 : q80 ? GEMM_Q80 : GEMM_Q8K;
+  const bool split = type == TPT_TYPE_F16 && act_mode == TPT_ACT_Q8;
   g.wtype = type;
   g.w = (const uint8_t*)w;
   g.w_stride = row_bytes(type, K);
@@ -356,10 +374,14 @@ int gemm_prepare(tpt_ctx* c, int type, const void* w, const float* x, float* y, 
   ActPrepArgs p;
   p.M = M; p.K = K; p.ldx = K; p.x = x; p.mode = g.mode;
   const size_t mk = (size_t)M * K;
-  // fp16 rows [M][K], then (GEMM_Q8K) block scales [M][K/256] and per-16 sums [M][K/16]
+  // fp16 rows [M][K], then GEMM_Q8K block scales [M][K/256] and per-16 sums [M][K/16], GEMM_Q80
+  // block scales [M][K/32], or (F16 weights, two passes) the fp16 remainder rows [M][K]
   const size_t o_d = (mk * 2 + 255) & ~(size_t)255;
-  const size_t o_s = o_d + (((size_t)M * (K / 256) * 4 + 255) & ~(size_t)255);
-  const size_t act_bytes = g.mode == GEMM_Q8K ? o_s + (size_t)M * (K / 16) * 2 : mk * 2;
+  const size_t nd = g.mode == GEMM_Q80 ? (size_t)M * (K / 32) : (size_t)M * (K / 256);
+  const size_t o_s = o_d + ((nd * 4 + 255) & ~(size_t)255);
+  const size_t act_bytes = g.mode == GEMM_Q8K ? o_s + (size_t)M * (K / 16) * 2
+                           : g.mode == GEMM_Q80 ? o_s
+                           : split ? o_d + mk * 2 : mk * 2;
   // split-K workspace when the output tiles cannot fill the device
   const int ns = gemm_splits(M, N, K);
   const size_t o_p = (act_bytes + 255) & ~(size_t)255;
@@ -371,10 +393,17 @@ int gemm_prepare(tpt_ctx* c, int type, const void* w, const float* x, float* y, 
   uint8_t* base = (uint8_t*)call->scratch;
   p.af = (uint16_t*)base;
   g.af = p.af;
-  if (g.mode == GEMM_Q8K) {
+  if (g.mode == GEMM_Q8K || g.mode == GEMM_Q80) {
     p.ad = (float*)(base + o_d);
+    g.ad = p.ad;
+  }
+  if (g.mode == GEMM_Q8K) {
     p.as16 = (int16_t*)(base + o_s);
-    g.ad = p.ad; g.as16 = p.as16;
+    g.as16 = p.as16;
+  }
+  if (split) {
+    p.af2 = (uint16_t*)(base + o_d);
+    call->lo = p.af2;
   }
   int rc = launch_act_prep(p, c->stream);
   if (rc) (void)hipFreeAsync(call->scratch, c->stream);
@@ -388,7 +417,7 @@ int tpt_gemm(tpt_ctx* c, int type, const void* w, const float* x, float* y, int 
   GemmCall call;
   int rc = gemm_prepare(c, type, w, x, y, M, K, N, act_mode, &call);
   if (rc) return rc;
-  rc = launch_gemm(call.g, c->stream);
+  rc = gemm_run(call, c->stream);
   (void)hipFreeAsync(call.scratch, c->stream);
   return rc;
 }
@@ -405,7 +434,7 @@ int tpt_bench_gemm(tpt_ctx* c, int type, const void* w, const float* x, float* y
   for (auto& v : ev)
     if (e == hipSuccess) e = hipEventCreate(&v);
   for (int i = 0; i < iters && rc == TPT_OK && e == hipSuccess; i++)
-    rc = launch_gemm_timed(call.g, c->stream, ev[2 * i], ev[2 * i + 1]);
+    rc = gemm_run(call, c->stream, ev[2 * i], ev[2 * i + 1]);
   if (e == hipSuccess && rc == TPT_OK) e = hipEventSynchronize(ev.back());
   float total = 0.f;
   for (int i = 0; i < iters && e == hipSuccess && rc == TPT_OK; i++) {

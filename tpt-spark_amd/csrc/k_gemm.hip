@@ -21,8 +21,15 @@
 //    Q5_K weights (vec_dot_q5k_q8k: Q4_K's arithmetic with 5-bit q): w = sc_j * q <= 63 * 31 is
 //    exact in fp16, but 128-element chains could pass 2^24, so w takes Q6_K's split (w = 64 w1 +
 //    w0, two chains over the super-block) and the mins term Q4_K's K=16 MFMA.
+//  * GEMM_Q80 (Q8_0 and Q4_0 weights: vec_dot_q8_0_q8_0 / vec_dot_q4_0_q8_0): the activation
+//    arrives as Q8_0 rows (int8 q, f16-rounded d per 32); the weight tile holds the exact integers
+//    q (Q8_0) or q - 8 (Q4_0).  One MFMA chain per 32-element block (|sum| <= 32 * 127 * 128,
+//    exact), scaled per block as candle does, y += (isum * d_w) * d_x.
 //  * GEMM_F16: the tile is dequantized into LDS as fp16 (Q4_K: d*sc*q - dmin*m, Q6_K:
-//    d*sc*(q - 32), rounded to fp16), the activation is fp16, one fp32 MFMA chain over all of K.
+//    d*sc*(q - 32), rounded to fp16; F16 weights as stored), the activation is fp16, one fp32
+//    MFMA chain over all of K.  For F16 weights candle multiplies in f32: the caller runs the
+//    GEMM twice, on x's fp16 rounding and on the fp16 rounding of the remainder (products exact
+//    in the f32 accumulator, x carried to 2^-22 relative).
 // Tiling (MI355X: 160 KB LDS, wave64, v_mfma_f32_32x32x16_f16): 512 threads, a 128 x 128 tile
 // of Y per workgroup, each wave 64 x 32 (2 x 1 MFMA tiles), two waves per SIMD so that one
 // wave's weight decode and block scaling run while the other's MFMAs do.  K advances half a super-block (128)
@@ -66,9 +73,14 @@ struct GemmBlock {               // GEMM_Q8K: one super-block's per-row and per-
   float dx[BM];                  // activation block scale
   float dw[BN], dm[BN];          // weight d, dmin
 };
+struct GemmQ80 {                 // GEMM_Q80: one K step's block scales (4 blocks of 32)
+  __attribute__((aligned(16))) float dwT[BN][4];  // weight d per tile column and block
+  __attribute__((aligned(16))) float dxT[4][BM];  // activation d per block and tile row
+};
 struct GemmSmem {
   GemmTile t[2];                 // by step parity: the half of the super-block
   GemmBlock blk[2];              // by super-block parity
+  GemmQ80 q80[2];                // by step parity
 };
 
 // Registers one thread stages for a K step (thread = row r = tid / 4, quarter qt = tid % 4 of
@@ -104,6 +116,24 @@ template <> struct Stage<TPT_TYPE_Q5_K> {
   u32x4 qh;
   u32x2 a16;
   float dx;
+};
+// Q8_0 / Q4_0: the 32-element block kb * 8 + 4 HB + qt of the row (its d, its quants) and the
+// activation block's d; F16: the 32 weights as stored.
+template <> struct Stage<TPT_TYPE_Q8_0> {
+  u32x4 a[4];
+  u32x4 q[2];
+  uint32_t d;
+  float dx;
+};
+template <> struct Stage<TPT_TYPE_Q4_0> {
+  u32x4 a[4];
+  u32x4 q;
+  uint32_t d;
+  float dx;
+};
+template <> struct Stage<TPT_TYPE_F16> {
+  u32x4 a[4];
+  u32x4 w[4];
 };
 
 // Q4_K and Q5_K share the header (d, dmin, packed scales and mins) and the per-16 mins term
@@ -141,6 +171,21 @@ __device__ __forceinline__ void stage_load(const GemmArgs& g, int m0, int n0, in
     st.q = *(const u32x4*)(blk + 16 + 32 * (2 * HB + (qt >> 1)) + 16 * (qt & 1));
     if constexpr (MODE == GEMM_Q8K && HB == 0)
       st.a16 = *(const u32x2*)(g.as16 + (size_t)m * (g.K / 16) + kb * 16 + 4 * qt);
+  } else if constexpr (WT == TPT_TYPE_Q8_0 || WT == TPT_TYPE_Q4_0) {
+    const int bi = kb * 8 + 4 * HB + qt;  // 34- / 18-byte blocks: 2-byte aligned
+    const uint8_t* blk = g.w + (size_t)n * g.w_stride + (size_t)bi * (WT == TPT_TYPE_Q8_0 ? 34 : 18);
+    st.d = ldg_u<uint16_t>(blk);
+    if constexpr (WT == TPT_TYPE_Q8_0) {
+      st.q[0] = ldg_u<u32x4>(blk + 2);
+      st.q[1] = ldg_u<u32x4>(blk + 18);
+    } else {
+      st.q = ldg_u<u32x4>(blk + 2);
+    }
+    st.dx = g.ad[(size_t)m * (g.K / 32) + bi];
+  } else if constexpr (WT == TPT_TYPE_F16) {
+    const u32x4* wr = (const u32x4*)(g.w + (size_t)n * g.w_stride + ((size_t)kb * 256 + 128 * HB + 32 * qt) * 2);
+#pragma unroll
+    for (int i = 0; i < 4; i++) st.w[i] = wr[i];
   } else if constexpr (WT == TPT_TYPE_Q5_K) {
     const uint8_t* blk = g.w + (size_t)n * g.w_stride + (size_t)kb * 176;
     st.h = *(const u32x4*)blk;
@@ -172,12 +217,42 @@ typedef _Float16 half2 __attribute__((ext_vector_type(2)));
 typedef short short2 __attribute__((ext_vector_type(2)));
 
 template <int WT, int MODE, int HB>
-__device__ __forceinline__ void stage_store(const Stage<WT>& st, GemmTile& T, GemmBlock& B) {
+__device__ __forceinline__ void stage_store(const Stage<WT>& st, GemmTile& T, GemmBlock& B, GemmQ80& Q) {
   const int tid = threadIdx.x, r = tid >> 2, qt = tid & 3;
 #pragma unroll
   for (int i = 0; i < 4; i++) *(u32x4*)&T.a[sw(r, 32 * qt + 8 * i)] = st.a[i];
-  float d, dmin = 0.f;
-  if constexpr (WT == TPT_TYPE_Q4_K) {
+  float d = 0.f, dmin = 0.f;
+  if constexpr (WT == TPT_TYPE_Q8_0 || WT == TPT_TYPE_Q4_0) {
+    // the block's 32 integers q (Q8_0) or q - 8 (Q4_0, element j < 16: low nibble of qs[j],
+    // j + 16: its high nibble) as exact fp16: a biased byte ORed into the mantissa of 1024.0
+    // and the bias subtracted in packed fp16
+    const half2 bias = WT == TPT_TYPE_Q8_0 ? half2{(_Float16)1152.f, (_Float16)1152.f}
+                                           : half2{(_Float16)1032.f, (_Float16)1032.f};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {  // elements 8c .. 8c + 7 of the block
+      u32x4 o;
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        uint32_t x;
+        if constexpr (WT == TPT_TYPE_Q8_0) {
+          x = st.q[c >> 1][2 * (c & 1) + h] ^ 0x80808080u;  // int8 + 128
+        } else {
+          const uint32_t wq = st.q[2 * (c & 1) + h];
+          x = (c < 2 ? wq : wq >> 4) & 0x0F0F0F0Fu;
+        }
+        const uint32_t p01 = __builtin_amdgcn_perm(0u, x, 0x0c010c00u) | 0x64006400u;
+        const uint32_t p23 = __builtin_amdgcn_perm(0u, x, 0x0c030c02u) | 0x64006400u;
+        o[2 * h] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, p01) - bias);
+        o[2 * h + 1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, p23) - bias);
+      }
+      *(u32x4*)&T.b[sw(r, 32 * qt + 8 * c)] = o;
+    }
+    Q.dwT[r][qt] = h2f((uint16_t)st.d);
+    Q.dxT[qt][r] = st.dx;
+  } else if constexpr (WT == TPT_TYPE_F16) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) *(u32x4*)&T.b[sw(r, 32 * qt + 8 * c)] = st.w[c];
+  } else if constexpr (WT == TPT_TYPE_Q4_K) {
     // weight row r, group g = 2 HB + qt / 2: qs[32g + l] holds element 64g + l (low nibble,
     // sub-block 2g) and 64g + 32 + l (high nibble, sub-block 2g + 1); this thread has
     // l = 16 (qt % 2) .. + 15, tile columns c0 + l' and c0 + 32 + l'
@@ -399,6 +474,41 @@ __device__ __forceinline__ void mfma_step(const GemmTile& T, floatx16 (&acc)[2],
   }
 }
 
+// GEMM_Q80: one K step = four 32-element blocks; per block one exact chain of two MFMAs, then
+// y += (isum * d_w) * d_x per element (the last multiply fused with the add).
+__device__ __forceinline__ void mfma_step_q80(const GemmTile& T, const GemmQ80& Q, floatx16 (&out)[2]) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wm = wid >> 2, wn = wid & 3;
+  const int lr = lane & 31, lk = 8 * (lane >> 5);
+  const float4 dw4 = *(const float4*)&Q.dwT[32 * wn + lr][0];
+  const float dw[4] = {dw4.x, dw4.y, dw4.z, dw4.w};
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    floatx16 c[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+      const int kk = 32 * j + 16 * t;
+      half8 a[2];
+#pragma unroll
+      for (int i = 0; i < 2; i++) a[i] = *(const half8*)&T.a[sw(64 * wm + 32 * i + lr, kk + lk)];
+      const half8 b = *(const half8*)&T.b[sw(32 * wn + lr, kk + lk)];
+#pragma unroll
+      for (int i = 0; i < 2; i++) c[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b, t == 0 ? floatx16{} : c[i], 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      float dxs[16];
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const float4 v = *(const float4*)&Q.dxT[j][64 * wm + 32 * i + q * 8 + (lane >> 5) * 4];
+        dxs[4 * q] = v.x; dxs[4 * q + 1] = v.y; dxs[4 * q + 2] = v.z; dxs[4 * q + 3] = v.w;
+      }
+#pragma unroll
+      for (int e = 0; e < 16; e++) out[i][e] = fmaf(c[i][e] * dw[j], dxs[e], out[i][e]);
+    }
+  }
+}
+
 // GEMM_Q8K end of a super-block, per element in f32: candle's y += d_x (d_w isum - dmin_w msum)
 // with the integers exact (the same terms as candle's (d_w d_x) isum - (dmin_w d_x) msum; the
 // f32 roundings differ by an ulp).  Q4_K: isum = the two exact 128-element chains added once,
@@ -472,7 +582,7 @@ __global__ void __launch_bounds__(GT, 1) gemm_kernel(const GemmArgs g) {
   // prologue: step 0 in LDS, step 1 in registers
   Stage<WT> st;
   stage_load<WT, MODE, 0>(g, m0, n0, kb0, st);
-  stage_store<WT, MODE, 0>(st, s.t[0], s.blk[kb0 & 1]);
+  stage_store<WT, MODE, 0>(st, s.t[0], s.blk[kb0 & 1], s.q80[0]);
   stage_load<WT, MODE, 1>(g, m0, n0, kb0, st);
   __syncthreads();
   for (int kb = kb0; kb < nkb; kb++) {
@@ -481,17 +591,20 @@ __global__ void __launch_bounds__(GT, 1) gemm_kernel(const GemmArgs g) {
     const int kn = kb + 1 < nkb ? kb + 1 : kb;
     // first half of super-block kb (tile t[0]): stage the second half, fetch the next block's
     // first half
-    stage_store<WT, MODE, 1>(st, s.t[1], s.blk[kb & 1]);
+    stage_store<WT, MODE, 1>(st, s.t[1], s.blk[kb & 1], s.q80[1]);
     stage_load<WT, MODE, 0>(g, m0, n0, kn, st);
     if constexpr (MODE == GEMM_Q8K) mfma_step<WT, MODE, true>(s.t[0], acc0, acc1);
+    else if constexpr (MODE == GEMM_Q80) mfma_step_q80(s.t[0], s.q80[0], out);
     else mfma_step<WT, MODE>(s.t[0], out, out);
     __syncthreads();
     // second half (tile t[1]): stage the next block's first half, fetch its second half
-    stage_store<WT, MODE, 0>(st, s.t[0], s.blk[(kb + 1) & 1]);
+    stage_store<WT, MODE, 0>(st, s.t[0], s.blk[(kb + 1) & 1], s.q80[0]);
     stage_load<WT, MODE, 1>(g, m0, n0, kn, st);
     if constexpr (MODE == GEMM_Q8K) {
       if constexpr (Q6) mfma_step<WT, MODE>(s.t[1], acc0, acc1);
       else mfma_step<WT, MODE, true>(s.t[1], acc1, acc1);
+    } else if constexpr (MODE == GEMM_Q80) {
+      mfma_step_q80(s.t[1], s.q80[1], out);
     } else {
       mfma_step<WT, MODE>(s.t[1], out, out);
     }
@@ -575,6 +688,7 @@ __global__ void __launch_bounds__(256) act_prep_kernel(const ActPrepArgs a) {
       v.w = v.w / rms * w.w;
     }
     const float e[4] = {v.x, v.y, v.z, v.w};
+    uint2* dst = (uint2*)(a.af + (size_t)m * K + (size_t)b * 256) + lane;
     if (a.mode == GEMM_Q8K) {  // the int8 values, stored as (exact) fp16 for the MFMA operand
       int qsum;
       float d;
@@ -582,14 +696,34 @@ __global__ void __launch_bounds__(256) act_prep_kernel(const ActPrepArgs a) {
       uint2 h;
       h.x = (uint32_t)f2h((float)(int8_t)(packed & 0xff)) | ((uint32_t)f2h((float)(int8_t)((packed >> 8) & 0xff)) << 16);
       h.y = (uint32_t)f2h((float)(int8_t)((packed >> 16) & 0xff)) | ((uint32_t)f2h((float)(int8_t)(packed >> 24)) << 16);
-      ((uint2*)(a.af + (size_t)m * K + (size_t)b * 256))[lane] = h;
+      *dst = h;
       if ((lane & 3) == 0) a.as16[(size_t)m * (K / 16) + b * 16 + (lane >> 2)] = (int16_t)qsum;
       if (lane == 0) a.ad[(size_t)m * nb + b] = d;
+    } else if (a.mode == GEMM_Q80) {
+      // BlockQ8_0::from_float per 32 (8 lanes): d = amax / 127 (stored rounded to f16),
+      // q = round(x / d) through id = 1 / d of the unrounded d -- the decode GEMV's prologue
+      float amax = fmaxf(fmaxf(fabsf(e[0]), fabsf(e[1])), fmaxf(fabsf(e[2]), fabsf(e[3])));
+      amax = fmaxf(amax, dpp_mov<0xB1>(amax));   // max over the 8 lanes of the block
+      amax = fmaxf(amax, dpp_mov<0x4E>(amax));
+      amax = fmaxf(amax, dpp_mov<0x141>(amax));
+      const float d = amax / 127.f;
+      const float id = d != 0.f ? 1.f / d : 0.f;
+      uint16_t q[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) q[j] = f2h(fminf(fmaxf(roundf(e[j] * id), -128.f), 127.f));
+      *dst = make_uint2((uint32_t)q[0] | ((uint32_t)q[1] << 16), (uint32_t)q[2] | ((uint32_t)q[3] << 16));
+      if ((lane & 7) == 0) a.ad[(size_t)m * (K / 32) + b * 8 + (lane >> 3)] = h2f(f2h(d));
     } else {
-      uint2 h;
-      h.x = (uint32_t)f2h(e[0]) | ((uint32_t)f2h(e[1]) << 16);
-      h.y = (uint32_t)f2h(e[2]) | ((uint32_t)f2h(e[3]) << 16);
-      ((uint2*)(a.af + (size_t)m * K + (size_t)b * 256))[lane] = h;
+      uint16_t h[4], l[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        h[j] = f2h(e[j]);
+        l[j] = f2h(e[j] - h2f(h[j]));  // exact difference, rounded once
+      }
+      *dst = make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+      if (a.af2)
+        ((uint2*)(a.af2 + (size_t)m * K + (size_t)b * 256))[lane] =
+            make_uint2((uint32_t)l[0] | ((uint32_t)l[1] << 16), (uint32_t)l[2] | ((uint32_t)l[3] << 16));
     }
   }
 }
@@ -599,7 +733,9 @@ __global__ void __launch_bounds__(256) act_prep_kernel(const ActPrepArgs a) {
 int launch_act_prep(const ActPrepArgs& a, hipStream_t s) {
   if (a.M <= 0 || a.K <= 0 || a.K % 256 || a.ldx < a.K || a.ldx % 4) return fail(TPT_ERR_INVALID, "act_prep: bad shape");
   if (!a.x) return fail(TPT_ERR_INVALID, "act_prep: null input");
-  if (!a.af || (a.mode == GEMM_Q8K && (!a.ad || !a.as16))) return fail(TPT_ERR_INVALID, "act_prep: null output");
+  if (a.mode != GEMM_Q8K && a.mode != GEMM_F16 && a.mode != GEMM_Q80) return fail(TPT_ERR_INVALID, "act_prep: bad mode");
+  if (!a.af || (a.mode == GEMM_Q8K && (!a.ad || !a.as16)) || (a.mode == GEMM_Q80 && !a.ad))
+    return fail(TPT_ERR_INVALID, "act_prep: null output");
   hipLaunchKernelGGL(act_prep_kernel, dim3((unsigned)a.M), dim3(256), 0, s, a);
   TPT_HIP(hipGetLastError());
   return TPT_OK;
@@ -609,19 +745,24 @@ int launch_gemm(const GemmArgs& g, hipStream_t s) { return launch_gemm_timed(g, 
 
 int launch_gemm_timed(const GemmArgs& g, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.K % 256) return fail(TPT_ERR_INVALID, "gemm: K must be a positive multiple of 256, M and N positive");
-  if (g.wtype != TPT_TYPE_Q4_K && g.wtype != TPT_TYPE_Q5_K && g.wtype != TPT_TYPE_Q6_K)
-    return fail(TPT_ERR_UNSUPPORTED, "gemm: weight type must be Q4_K, Q5_K or Q6_K");
-  if (g.mode != GEMM_Q8K && g.mode != GEMM_F16) return fail(TPT_ERR_INVALID, "gemm: bad activation mode");
+  const bool kq = g.wtype == TPT_TYPE_Q4_K || g.wtype == TPT_TYPE_Q5_K || g.wtype == TPT_TYPE_Q6_K;
+  const bool q80 = g.wtype == TPT_TYPE_Q8_0 || g.wtype == TPT_TYPE_Q4_0;
+  if (!kq && !q80 && g.wtype != TPT_TYPE_F16)
+    return fail(TPT_ERR_UNSUPPORTED, "gemm: weight type must be Q4_K, Q5_K, Q6_K, Q8_0, Q4_0 or F16");
+  if ((kq && g.mode != GEMM_Q8K && g.mode != GEMM_F16) || (q80 && g.mode != GEMM_Q80) ||
+      (g.wtype == TPT_TYPE_F16 && g.mode != GEMM_F16))
+    return fail(TPT_ERR_INVALID, "gemm: activation mode does not match the weight type");
   if (!g.w || !g.y) return fail(TPT_ERR_INVALID, "gemm: null weight/output pointer");
   if (!g.af) return fail(TPT_ERR_INVALID, "gemm: null activation rows");
-  if (g.mode == GEMM_Q8K && (!g.ad || (g.wtype != TPT_TYPE_Q6_K && !g.as16)))
-    return fail(TPT_ERR_INVALID, "gemm: Q8_K mode needs block scales (and per-16 sums for Q4_K and Q5_K)");
-  if (g.w_stride < (size_t)(g.K / 256) * type_bytes(g.wtype))
+  if ((g.mode == GEMM_Q8K && (!g.ad || (g.wtype != TPT_TYPE_Q6_K && !g.as16))) || (g.mode == GEMM_Q80 && !g.ad))
+    return fail(TPT_ERR_INVALID, "gemm: quantized activations need block scales (and per-16 sums for Q4_K and Q5_K)");
+  if (g.w_stride < row_bytes(g.wtype, g.K))
     return fail(TPT_ERR_INVALID, "gemm: weight row stride shorter than a row");
-  if (g.wtype != TPT_TYPE_Q6_K && ((g.w_stride % 16) || ((uintptr_t)g.w % 16)))
-    return fail(TPT_ERR_INVALID, "gemm: Q4_K and Q5_K weight rows must be 16-byte aligned");
-  if (g.wtype == TPT_TYPE_Q6_K && ((g.w_stride % 2) || ((uintptr_t)g.w % 2)))
-    return fail(TPT_ERR_INVALID, "gemm: Q6_K weight rows must be 2-byte aligned");
+  const bool a16 = g.wtype == TPT_TYPE_Q4_K || g.wtype == TPT_TYPE_Q5_K || g.wtype == TPT_TYPE_F16;
+  if (a16 && ((g.w_stride % 16) || ((uintptr_t)g.w % 16)))
+    return fail(TPT_ERR_INVALID, "gemm: Q4_K, Q5_K and F16 weight rows must be 16-byte aligned");
+  if (!a16 && ((g.w_stride % 2) || ((uintptr_t)g.w % 2)))
+    return fail(TPT_ERR_INVALID, "gemm: Q6_K, Q8_0 and Q4_0 weight rows must be 2-byte aligned");
   int ns = gemm_splits(g.M, g.N, g.K);
   if (!g.part || g.part_floats < (size_t)ns * g.M * g.N) ns = 1;  // no workspace: one pass over K
   const dim3 grid((unsigned)((g.N + BN - 1) / BN), (unsigned)((g.M + BM - 1) / BM), (unsigned)ns);
@@ -632,6 +773,12 @@ int launch_gemm_timed(const GemmArgs& g, hipStream_t s, hipEvent_t ev0, hipEvent
   } else if (g.wtype == TPT_TYPE_Q5_K) {
     if (g.mode == GEMM_Q8K) hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q5_K, GEMM_Q8K>), grid, dim3(GT), 0, s, ev0, e1, 0, g);
     else hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q5_K, GEMM_F16>), grid, dim3(GT), 0, s, ev0, e1, 0, g);
+  } else if (g.wtype == TPT_TYPE_Q8_0) {
+    hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q8_0, GEMM_Q80>), grid, dim3(GT), 0, s, ev0, e1, 0, g);
+  } else if (g.wtype == TPT_TYPE_Q4_0) {
+    hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q4_0, GEMM_Q80>), grid, dim3(GT), 0, s, ev0, e1, 0, g);
+  } else if (g.wtype == TPT_TYPE_F16) {
+    hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_F16, GEMM_F16>), grid, dim3(GT), 0, s, ev0, e1, 0, g);
   } else {
     if (g.mode == GEMM_Q8K) hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q6_K, GEMM_Q8K>), grid, dim3(GT), 0, s, ev0, e1, 0, g);
     else hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q6_K, GEMM_F16>), grid, dim3(GT), 0, s, ev0, e1, 0, g);

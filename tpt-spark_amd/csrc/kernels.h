@@ -57,16 +57,20 @@ int launch_gemv_q8(const tpt_ctx* ctx, int wtype, const GemvArgs& a, hipStream_t
 int launch_gemv_f32(int wtype, const uint8_t* w, const float* x, float* y, int K, int N,
                     hipStream_t s);
 
-// ---- prefill GEMM (k_gemm.hip): Y[M,N] = X[M,K] . W[N,K]^T, W in Q4_K, Q5_K or Q6_K blocks
-enum GemmMode { GEMM_Q8K = 0, GEMM_F16 = 1 };
+// ---- prefill GEMM (k_gemm.hip): Y[M,N] = X[M,K] . W[N,K]^T, W in Q4_K, Q5_K, Q6_K, Q8_0, Q4_0
+// or F16 rows.  Modes: GEMM_Q8K (k-quant weights, Q8_K activation rows), GEMM_Q80 (Q8_0 / Q4_0
+// weights, Q8_0 activation rows), GEMM_F16 (fp16 activation rows; k-quants dequantized to fp16,
+// F16 weights as stored).
+enum GemmMode { GEMM_Q8K = 0, GEMM_F16 = 1, GEMM_Q80 = 2 };
 struct GemmArgs {
   int M = 0, N = 0, K = 0, mode = GEMM_Q8K;
-  int wtype = TPT_TYPE_Q4_K;         // weight blocks: TPT_TYPE_Q4_K, TPT_TYPE_Q5_K or TPT_TYPE_Q6_K
+  int wtype = TPT_TYPE_Q4_K;         // weight rows: Q4_K, Q5_K, Q6_K (GEMM_Q8K / GEMM_F16), Q8_0,
+                                     // Q4_0 (GEMM_Q80), F16 (GEMM_F16)
   const uint8_t* w = nullptr;
   size_t w_stride = 0;               // bytes per weight row
-  const uint16_t* af = nullptr;      // [M][K] fp16 bits (GEMM_Q8K: the Q8_K int8 values, exact)
-  const float* ad = nullptr;         // GEMM_Q8K: [M][K/256] block scales
-  const int16_t* as16 = nullptr;     //           [M][K/16] per-16 sums
+  const uint16_t* af = nullptr;      // [M][K] fp16 bits (GEMM_Q8K / GEMM_Q80: the int8 values, exact)
+  const float* ad = nullptr;         // GEMM_Q8K: [M][K/256] block scales; GEMM_Q80: [M][K/32]
+  const int16_t* as16 = nullptr;     // GEMM_Q8K: [M][K/16] per-16 sums
   float* y = nullptr;
   int ldy = 0;
   const float* resid = nullptr;      // optional: y = X.W^T + resid
@@ -82,7 +86,9 @@ int launch_gemm(const GemmArgs& g, hipStream_t s);
 int launch_gemm_timed(const GemmArgs& g, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1);
 
 // Activation rows for the prefill GEMM: optional RMSNorm (w, eps) or SwiGLU (silu(x) * x2),
-// then Q8_K quantization (the int8 values as fp16 in af, with ad/as16) or fp16 conversion (af).
+// then Q8_K quantization (GEMM_Q8K: the int8 values as fp16 in af, with ad / as16), Q8_0
+// quantization (GEMM_Q80: af, ad per 32) or fp16 conversion (GEMM_F16: af; with af2 also the
+// remainder x - af rounded to fp16, so that af + af2 carries x to 2^-22 relative).
 // x rows of K floats, stride ldx.
 struct ActPrepArgs {
   int M = 0, K = 0, ldx = 0;
@@ -94,6 +100,7 @@ struct ActPrepArgs {
   float* ad = nullptr;
   int16_t* as16 = nullptr;
   uint16_t* af = nullptr;
+  uint16_t* af2 = nullptr;           // GEMM_F16: optional fp16 remainder rows
 };
 int launch_act_prep(const ActPrepArgs& a, hipStream_t s);
 

@@ -328,10 +328,11 @@ int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_t
   }
   TPT_HIP(hipHostMalloc((void**)&st_host, sizeof(StepState)));
   TPT_HIP(hipHostMalloc((void**)&ids_host, (size_t)max_ctx * 4));
+  // every layer matrix type has a GEMM form: the batched prefill is the default
   batched_prefill = true;
+  has_f16_matrix = false;
   for (const Layer& L : layers)
-    for (int t : {L.tq, L.tk, L.tv, L.to, L.tg, L.tu, L.td})
-      if (t != TPT_TYPE_Q4_K && t != TPT_TYPE_Q5_K && t != TPT_TYPE_Q6_K) batched_prefill = false;
+    for (int t : {L.tq, L.tk, L.tv, L.to, L.tg, L.tu, L.td}) has_f16_matrix |= t == TPT_TYPE_F16;
   const char* ev_pf = getenv("TPT_HIP_PREFILL");
   if (ev_pf && strcmp(ev_pf, "steps") == 0) batched_prefill = false;
   const char* ev_att = getenv("TPT_HIP_CAUSAL_ATTN");
@@ -654,7 +655,8 @@ int tpt_model::prefill_scratch(int T, int n_chunks) {
   size_t off = 0;
   auto carve = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes, 256); return o; };
   const size_t o_x = carve((size_t)T * H * 4), o_af = carve((size_t)T * Kmax * 2),
-               o_ad = carve((size_t)T * (Kmax / 256) * 4), o_as = carve((size_t)T * (Kmax / 16) * 2),
+               o_af2 = carve(has_f16_matrix ? (size_t)T * Kmax * 2 : 0),
+               o_ad = carve((size_t)T * (Kmax / 32) * 4), o_as = carve((size_t)T * (Kmax / 16) * 2),
                o_qkv = carve((size_t)T * (qd + 2 * kd) * 4), o_q = carve((size_t)T * qd * 4),
                o_att = carve((size_t)T * qd * 4), o_g = carve((size_t)T * F * 4), o_u = carve((size_t)T * F * 4),
                o_part = carve((size_t)T * attn_part_floats(desc.n_heads, desc.n_kv_heads, desc.head_dim, n_chunks) * 4),
@@ -680,6 +682,7 @@ int tpt_model::prefill_scratch(int T, int n_chunks) {
   uint8_t* b = (uint8_t*)pf_mem;
   pf_x = (float*)(b + o_x);
   pf_af = (uint16_t*)(b + o_af);
+  pf_af2 = has_f16_matrix ? (uint16_t*)(b + o_af2) : nullptr;
   pf_ad = (float*)(b + o_ad);
   pf_as16 = (int16_t*)(b + o_as);
   pf_qkv = (float*)(b + o_qkv);
@@ -724,32 +727,51 @@ int tpt_model::batched_layers(int T, int p0, int l0, int l1) {
   const size_t layer_kv = (size_t)2 * nkv * mc * hd;
   const int Lmax = p0 + T, nch = slice_chunks(Lmax), cl = attn_chunk_len(Lmax, nch);
   int rc;
-  auto prep = [&](const float* xx, const float* x2, int K, const float* nw) {
+  // candle's arithmetic per weight type: Q8_K activation rows for the k-quants, Q8_0 rows for
+  // Q8_0 / Q4_0, f32 for F16 (fp16 rounding plus remainder, two GEMM passes)
+  auto mode_of = [](int type) {
+    return type == TPT_TYPE_F16 ? GEMM_F16 : type == TPT_TYPE_Q8_0 || type == TPT_TYPE_Q4_0 ? GEMM_Q80 : GEMM_Q8K;
+  };
+  // activation rows of (x, x2, norm) in the mode the next GEMM needs; rows already prepared
+  // for the same input and mode are reused
+  struct Prepared { const float* x; const float* x2; const float* nw; int K, mode; } last{nullptr, nullptr, nullptr, 0, -1};
+  auto prep = [&](const float* xx, const float* x2, int K, const float* nw, int type) {
+    const int mode = mode_of(type);
+    if (last.x == xx && last.x2 == x2 && last.nw == nw && last.K == K && last.mode == mode) return (int)TPT_OK;
     ActPrepArgs a;
     a.M = T; a.K = K; a.ldx = K; a.x = xx; a.x2 = x2; a.norm_w = nw; a.eps = desc.rms_eps;
-    a.mode = GEMM_Q8K; a.af = pf_af; a.ad = pf_ad; a.as16 = pf_as16;
+    a.mode = mode; a.af = pf_af; a.ad = pf_ad; a.as16 = pf_as16;
+    a.af2 = mode == GEMM_F16 ? pf_af2 : nullptr;
+    last = {xx, x2, nw, K, mode};
     return launch_act_prep(a, stream);
   };
   auto gemm = [&](int type, const uint8_t* w, int K, int N, float* y, int ldy, const float* resid) {
     GemmArgs g;
-    g.M = T; g.N = N; g.K = K; g.mode = GEMM_Q8K; g.wtype = type;
+    g.M = T; g.N = N; g.K = K; g.mode = mode_of(type); g.wtype = type;
     g.w = w; g.w_stride = row_bytes(type, K);
     g.af = pf_af; g.ad = pf_ad; g.as16 = pf_as16;
     g.y = y; g.ldy = ldy; g.resid = resid; g.ldr = ldy;
     g.part = pf_gsplit; g.part_floats = pf_gsplit_floats;
+    if (type != TPT_TYPE_F16) return launch_gemm(g, stream);
+    // y = W . lo (+ resid), then y = W . hi + y
+    g.af = pf_af2;
+    int r = launch_gemm(g, stream);
+    if (r) return r;
+    g.af = pf_af;
+    g.resid = y;
     return launch_gemm(g, stream);
   };
   for (int l = l0; l < l1; l++) {
     const Layer& L = layers[l];
     uint8_t* kc = (uint8_t*)kv + (size_t)l * layer_kv * kv_elem;
     uint8_t* vc = kc + (size_t)nkv * mc * hd * kv_elem;
-    if ((rc = prep(pf_x, nullptr, H, L.attn_norm))) return rc;
     const int ldq = qd + 2 * kd;
     if (L.qkv_adjacent) {
-      if ((rc = gemm(L.tq, L.q, H, ldq, pf_qkv, ldq, nullptr))) return rc;
+      if ((rc = prep(pf_x, nullptr, H, L.attn_norm, L.tq)) || (rc = gemm(L.tq, L.q, H, ldq, pf_qkv, ldq, nullptr))) return rc;
     } else {
-      if ((rc = gemm(L.tq, L.q, H, qd, pf_qkv, ldq, nullptr)) || (rc = gemm(L.tk, L.k, H, kd, pf_qkv + qd, ldq, nullptr)) ||
-          (rc = gemm(L.tv, L.v, H, kd, pf_qkv + qd + kd, ldq, nullptr)))
+      if ((rc = prep(pf_x, nullptr, H, L.attn_norm, L.tq)) || (rc = gemm(L.tq, L.q, H, qd, pf_qkv, ldq, nullptr)) ||
+          (rc = prep(pf_x, nullptr, H, L.attn_norm, L.tk)) || (rc = gemm(L.tk, L.k, H, kd, pf_qkv + qd, ldq, nullptr)) ||
+          (rc = prep(pf_x, nullptr, H, L.attn_norm, L.tv)) || (rc = gemm(L.tv, L.v, H, kd, pf_qkv + qd + kd, ldq, nullptr)))
         return rc;
     }
     QkvPostArgs qp;
@@ -764,11 +786,14 @@ int tpt_model::batched_layers(int T, int p0, int l0, int l1) {
     rc = causal_mfma && attn_causal_mfma_supported(at) ? launch_attn_causal_mfma(at, stream)
                                                        : launch_attn_decode(at, stream);
     if (rc) return rc;
-    if ((rc = prep(pf_att, nullptr, qd, nullptr)) || (rc = gemm(L.to, L.o, qd, H, pf_x, H, pf_x))) return rc;
-    if ((rc = prep(pf_x, nullptr, H, L.ffn_norm)) || (rc = gemm(L.tg, L.gate, H, F, pf_g, F, nullptr)) ||
-        (rc = gemm(L.tu, L.up, H, F, pf_u, F, nullptr)))
+    if ((rc = prep(pf_att, nullptr, qd, nullptr, L.to)) || (rc = gemm(L.to, L.o, qd, H, pf_x, H, pf_x))) return rc;
+    // pf_x changed in place: the rows prepared from it before are stale
+    last.mode = -1;
+    if ((rc = prep(pf_x, nullptr, H, L.ffn_norm, L.tg)) || (rc = gemm(L.tg, L.gate, H, F, pf_g, F, nullptr)) ||
+        (rc = prep(pf_x, nullptr, H, L.ffn_norm, L.tu)) || (rc = gemm(L.tu, L.up, H, F, pf_u, F, nullptr)))
       return rc;
-    if ((rc = prep(pf_g, pf_u, F, nullptr)) || (rc = gemm(L.td, L.down, F, H, pf_x, H, pf_x))) return rc;
+    if ((rc = prep(pf_g, pf_u, F, nullptr, L.td)) || (rc = gemm(L.td, L.down, F, H, pf_x, H, pf_x))) return rc;
+    last.mode = -1;
   }
   return TPT_OK;
 }

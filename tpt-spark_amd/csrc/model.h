@@ -72,6 +72,8 @@ struct tpt_model {
   float *pf_x = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_att = nullptr, *pf_g = nullptr,
         *pf_u = nullptr, *pf_part = nullptr, *pf_ad = nullptr;
   uint16_t* pf_af = nullptr;  // activation rows for the GEMMs (fp16)
+  uint16_t* pf_af2 = nullptr; // F16 layer matrices: the fp16 remainder rows
+  bool has_f16_matrix = false;
   int16_t* pf_as16 = nullptr;
   uint32_t* pf_ids = nullptr;
 
