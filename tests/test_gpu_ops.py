@@ -389,7 +389,7 @@ def gemm_case(ctx, M, K, N, seed, bf16=False, qtype=TYPE_Q4_K):
 
 
 @pytest.mark.parametrize("M,K,N", [(16, 256, 64), (33, 512, 300), (128, 4096, 4096), (200, 2048, 1000),
-                                   (130, 14336, 256)])
+                                   (130, 14336, 256), (300, 1024, 700)])
 @pytest.mark.parametrize("qtype", GEMV_TYPES)
 def test_gemm_q8k_matches_candle(ctx, M, K, N, qtype):
     """TPT_ACT_Q8: candle's prefill arithmetic for the weight type (each X row quantized to
@@ -465,6 +465,70 @@ def test_gemm_q5k_exact_at_integer_extremes(ctx):
     assert rel_l2(y, ref) < 1e-6
     yv = ctx.gemv(TYPE_Q5_K, ctx.to_device(w), ctx.to_device(x[7].copy()), K, N)
     assert rel_l2(y[7], yv) < 1e-6
+
+
+def q4k_extreme_blocks(n_blocks, seed):
+    """Q4_K blocks (d = 1, dmin = 0.25) with every scale and min 63: a third with all q = 0
+    (the integers sc * q - 480 of the 256-row tile at -480), a third with all q = 15 (945), a
+    third with random nibbles."""
+    rng = np.random.default_rng(seed)
+    b = rng.integers(0, 256, (n_blocks, 144), dtype=np.uint8)
+    b[:, 4:16] = 0xFF
+    b[0::3, 16:] = 0x00
+    b[1::3, 16:] = 0xFF
+    b[:, 0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    b[:, 2:4] = np.frombuffer(np.float16(0.25).tobytes(), np.uint8)
+    return b.reshape(-1)
+
+
+WIDE_CASES = [(256, 4096, 4096), (300, 512, 200), (520, 2048, 1000), (2048, 4096, 1024),
+              (2048, 4096, 4096), (256, 4096, 256)]
+
+
+def gemm_split_count(M, N, K, tile_m):
+    """The launcher's split-K count for a grid of tile_m x 128 tiles (k_gemm.hip splits_for)."""
+    tiles, nkb = -(-N // 128) * -(-M // tile_m), K // 256
+    return 1 if tiles > 128 or nkb < 4 else min(256 // tiles, nkb // 2, 8)
+
+
+@pytest.mark.parametrize("M,K,N", WIDE_CASES)
+@pytest.mark.parametrize("act", [tpthip.ACT_Q8, tpthip.ACT_F16])
+def test_gemm_wide_tiles_equal_narrow(ctx, monkeypatch, M, K, N, act):
+    """Q4_K over M >= 256 rows runs on 256 x 128 tiles (one exact chain per super-block on
+    w - 480, activation tiles by LDS DMA, last tiles shifted back inside the matrix); the
+    128 x 128 kernel computes every element with the same integers and f32 steps, so the two
+    agree bit for bit when both split K the same way (partial row and column tiles, 4 and 8
+    splits, none), and to f32 regrouping of the split sums otherwise; both modes."""
+    w, x = gemm_case(ctx, M, K, N, seed=M + 7 * N + K, qtype=TYPE_Q4_K)
+    wd, xd = ctx.to_device(w), ctx.to_device(x)
+    monkeypatch.setenv("TPT_HIP_GEMM_TILE", "narrow")
+    y0 = ctx.gemm(TYPE_Q4_K, wd, xd, M, K, N, act=act)
+    monkeypatch.delenv("TPT_HIP_GEMM_TILE")
+    y1 = ctx.gemm(TYPE_Q4_K, wd, xd, M, K, N, act=act)
+    if gemm_split_count(M, N, K, 128) == gemm_split_count(M, N, K, 256):
+        assert np.array_equal(y0.view(np.uint32), y1.view(np.uint32))
+    else:
+        assert rel_l2(y1, y0) < 1e-6
+
+
+def test_gemm_wide_exact_at_integer_extremes(ctx, monkeypatch):
+    """The 256-row tile's chain sum(q8 * (sc q - 480)) reaches its bound 256 * 128 * 480 < 2^24
+    for rows of +1 (Q8_K -128 everywhere) against q = 0 blocks of scale 63; with +-1 and 0.5
+    rows and q = 15 or random blocks the GEMM still equals the oracle's integers to f32
+    rounding and the 128 x 128 kernel bit for bit."""
+    M, K, N = 256, 1024, 128
+    w = q4k_extreme_blocks(N * K // 256, seed=8)
+    x = np.random.default_rng(9).choice(np.array([-1.0, 1.0, 0.5], np.float32), (M, K))
+    x[0::4] = 1.0
+    x[1::4] = -1.0
+    wd, xd = ctx.to_device(w), ctx.to_device(x)
+    monkeypatch.delenv("TPT_HIP_GEMM_TILE", raising=False)
+    y = ctx.gemm(TYPE_Q4_K, wd, xd, M, K, N, act=tpthip.ACT_Q8)
+    ref = oracle.matmul(TYPE_Q4_K, x, w, N)
+    assert rel_l2(y, ref) < 1e-6
+    monkeypatch.setenv("TPT_HIP_GEMM_TILE", "narrow")
+    y0 = ctx.gemm(TYPE_Q4_K, wd, xd, M, K, N, act=tpthip.ACT_Q8)
+    assert np.array_equal(y0.view(np.uint32), y.view(np.uint32))
 
 
 @pytest.mark.parametrize("M,N,qtype", [(128, 4096, TYPE_Q4_K), (512, 4096, TYPE_Q4_K), (2048, 4096, TYPE_Q4_K),

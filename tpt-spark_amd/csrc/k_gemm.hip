@@ -38,9 +38,14 @@
 // the Q4_K decode overlaps the matrix cores instead of alternating with them.  The activation
 // arrives as fp16 rows from act_prep_kernel (in GEMM_Q8K mode the int8 values, exact in fp16), so
 // no workgroup converts it again.
+// Q4_K GEMMs of at least 256 rows run on gemm_wide_kernel instead: 256 x 128 tiles, 64 x 64 per
+// wave, activation tiles fetched two steps ahead by LDS DMA, one exact chain per super-block on
+// the shifted integers sc * q - 480 (same results, bit for bit).
 #include <hip/hip_ext.h>
 
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
 
 #include "kernels.h"
 
@@ -631,6 +636,361 @@ __global__ void __launch_bounds__(GT, 1) gemm_kernel(const GemmArgs g) {
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Q4_K weights with M > 128: 256 x 128 tiles.  Each wave computes 64 x 64 of Y (2 x 2 MFMA
+// tiles), so a K step reads 4 KB of LDS operands per 4 MFMAs (the 128 x 128 kernel: 3 KB per 2)
+// and one decoded weight tile serves 256 activation rows.  K advances 64 per step, one Q4_K group
+// (the low and high nibbles of 32 qs bytes: sub-blocks 2g and 2g + 1), four steps per super-block,
+// through a double-buffered tile of 128-byte rows.
+// GEMM_Q8K: one exact chain per super-block.  The tile holds w - 480 for w = sc * q in [0, 945],
+// so every partial sum is an integer of magnitude at most 256 * 128 * 480 < 2^24 (exact in f32),
+// and isum = chain + 480 * sum(q8) is formed by one f32 add: the rounding of the exact integer,
+// the value the two half chains of the 128 x 128 kernel give.  The rest of the block arithmetic is
+// that kernel's, so both produce the same bits.
+constexpr int WBM = 256, WBN = 128, WBK = 64;
+constexpr int WOFF = 480;  // a multiple of 32: 1024 sc + WOFF is exact in fp16 up to sc = 63
+// Rows of 64 fp16 (128 bytes): the 16-byte chunk c of row r sits at c ^ f(r % 8) with f a
+// permutation, so the 8 rows one MFMA operand read covers per chunk column hit 8 distinct chunk
+// positions.  A rows: f = identity (each staging thread writes 4 chunks of one half of a row).
+// B rows: f(r) = 4 (r % 2) + (r / 2) % 4, so that the two rows one 8-lane store group covers (4
+// threads per row, one chunk each in a half of the row) land in opposite halves.
+__device__ __forceinline__ int swa(int r, int k) { return r * WBK + (((k >> 3) ^ (r & 7)) << 3); }
+__device__ __forceinline__ int swb(int r, int k) {
+  return r * WBK + (((k >> 3) ^ (((r & 1) << 2) | ((r >> 1) & 3))) << 3);
+}
+struct WideBlock {               // GEMM_Q8K: one super-block's per-row and per-column data
+  _Float16 a16[WBM][LDG];        // activation per-16 sums
+  _Float16 b16[WBN][LDG];        // weight mins, each repeated for its two 16-element halves
+  float dx[WBM];                 // activation block scale
+  float sx[WBM];                 // 480 * the activation row's sum of q8 over the super-block
+  float dw[WBN], dm[WBN];        // weight d, dmin
+};
+// 158 KB: activation tiles by step mod 3 (the DMA runs two steps ahead), weight tiles by step
+// parity, block data by super-block parity
+struct WideSmem {
+  __attribute__((aligned(16))) _Float16 a[3][WBM * WBK];
+  __attribute__((aligned(16))) _Float16 b[2][WBN * WBK];
+  WideBlock blk[2];
+};
+// Registers a thread stages for a K step: weight row tid / 4, qs bytes 8 (tid % 4) .. + 7 of the
+// step's group.  With the super-block's first step also that weight row's header (d, dmin,
+// scales: kept for the other three steps) and, in GEMM_Q8K mode, 8 of the per-16 sums of
+// activation row tid / 2 (sums 8 (tid % 2) .. + 7) and its block scale.  The activation tile
+// goes from memory to LDS directly (wide_dma_a).
+struct WideStage {
+  u32x2 q;
+  u32x4 h;
+  u32x4 a16;
+  float dx;
+};
+// A thread's byte offsets from the operand bases, fixed over the K loop (32-bit: the launcher
+// keeps every operand below 4 GiB, so loads take a uniform base plus one offset register): its
+// DMA lanes' offset within a group of 8 activation rows (row l / 8, chunk (l % 8) ^ (l / 8)),
+// its weight row, its activation row's per-16 sums and block scales.  The tile's rows and
+// columns all lie inside the matrices (the last tiles are shifted back, see gemm_wide_kernel),
+// so no index is clamped.
+struct WideOff {
+  uint32_t a, w, s16, sd;
+};
+__device__ __forceinline__ WideOff wide_offsets(const GemmArgs& g, int m0, int n0) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int p = lane & 7, rr = lane >> 3;
+  WideOff o;
+  o.a = (uint32_t)rr * (uint32_t)g.K * 2u + 16u * (uint32_t)(p ^ rr);
+  const uint32_t m = (uint32_t)(m0 + (tid >> 1)), n = (uint32_t)(n0 + (tid >> 2));
+  o.w = n * (uint32_t)g.w_stride;
+  o.s16 = m * (uint32_t)(g.K / 16) * 2u + 16u * (uint32_t)(tid & 1);
+  o.sd = m * (uint32_t)(g.K / 256) * 4u;
+  return o;
+}
+
+template <int MODE, int S>
+__device__ __forceinline__ void wide_load(const GemmArgs& g, const WideOff& o, int kb, WideStage& st) {
+  const uint32_t bo = o.w + (uint32_t)kb * 144u;
+  if constexpr (S == 0) st.h = *(const u32x4*)(g.w + bo);
+  st.q = *(const u32x2*)(g.w + (bo + 16u + 32u * S + 8u * (threadIdx.x & 3)));
+  if constexpr (MODE == GEMM_Q8K && S == 0) {
+    st.a16 = *(const u32x4*)((const char*)g.as16 + (o.s16 + (uint32_t)kb * 32u));
+    st.dx = *(const float*)((const char*)g.ad + (o.sd + (uint32_t)kb * 4u));
+  }
+}
+
+// The activation tile of step S of super-block kb, by LDS DMA (global_load_lds_dwordx4: lane l of
+// a wave writes the 16 bytes at LDS offset 16 l of the instruction's 1 KB): wave w's instruction i
+// fills rows 8 (4 w + i) .. + 7, lane l position l % 8 of row 8 (4 w + i) + l / 8, which holds
+// that row's chunk (l % 8) ^ (l / 8).  Complete once the wave's vector memory count drains.
+template <int S>
+__device__ __forceinline__ void wide_dma_a(const GemmArgs& g, const WideOff& o, int m0, int kb, _Float16* A) {
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar bases
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t r0 = (uint32_t)(m0 + 8 * (4 * w + i));  // the instruction's first row
+    const char* base = (const char*)g.af + (r0 * (uint32_t)g.K * 2u + (uint32_t)kb * 512u + 2u * WBK * S);
+    __builtin_amdgcn_global_load_lds(base + o.a, (__attribute__((address_space(3))) void*)&A[8 * WBK * (4 * w + i)], 16, 0, 0);
+  }
+}
+
+// s_waitcnt vmcnt(N): at most N of this wave's global loads (LDS DMA included) are in flight;
+// vector memory loads complete in issue order
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 16, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
+
+template <int MODE, int S>
+__device__ __forceinline__ void wide_store(const WideStage& st, _Float16* Bt, WideBlock& B) {
+  const int tid = threadIdx.x, ra = tid >> 1, ha = tid & 1, rb = tid >> 2, qt = tid & 3;
+  // qs byte 32 S + l holds element l of sub-block 2 S (low nibble) and of 2 S + 1 (high); this
+  // thread has l = 8 qt .. + 7: tile columns 8 qt .. and 32 + 8 qt ..
+  int sc0, m0, sc1, m1;
+  get_scale_min(st.h, 2 * S, &sc0, &m0);
+  get_scale_min(st.h, 2 * S + 1, &sc1, &m1);
+  const float d = h2f((uint16_t)(st.h.x & 0xffff)), dmin = h2f((uint16_t)(st.h.x >> 16));
+  if constexpr (MODE == GEMM_Q8K) {
+    // sc * q - 480 two at a time: (1024 + q) * sc - (1024 sc + 480) in one packed fp16 fma,
+    // whose single rounding lands on the exact integer (|sc q - 480| <= 480)
+    const half2 s0 = {(_Float16)sc0, (_Float16)sc0}, s1 = {(_Float16)sc1, (_Float16)sc1};
+    const half2 o0 = {(_Float16)(-1024 * sc0 - WOFF), (_Float16)(-1024 * sc0 - WOFF)};
+    const half2 o1 = {(_Float16)(-1024 * sc1 - WOFF), (_Float16)(-1024 * sc1 - WOFF)};
+    auto dec = [&](uint32_t pair, half2 sc, half2 off) {
+      const half2 v = __builtin_bit_cast(half2, (pair & 0x000F000Fu) | 0x64006400u);
+      return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(v, sc, off));
+    };
+    u32x4 lo, hi;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const uint32_t x = st.q[h];
+      const uint32_t p01 = __builtin_amdgcn_perm(0u, x, 0x0c010c00u);  // bytes 0, 1 -> halves
+      const uint32_t p23 = __builtin_amdgcn_perm(0u, x, 0x0c030c02u);  // bytes 2, 3 -> halves
+      lo[2 * h] = dec(p01, s0, o0);
+      lo[2 * h + 1] = dec(p23, s0, o0);
+      hi[2 * h] = dec(p01 >> 4, s1, o1);
+      hi[2 * h + 1] = dec(p23 >> 4, s1, o1);
+    }
+    *(u32x4*)&Bt[swb(rb, 8 * qt)] = lo;
+    *(u32x4*)&Bt[swb(rb, 32 + 8 * qt)] = hi;
+    if constexpr (S == 0) {
+      // the weight row's d, dmin and mins (this thread: sub-blocks 2 qt, 2 qt + 1); the four
+      // threads of the row store the same d and dmin
+      // get_scale_min_k4's mins for j = 2 qt + c: byte j of Z (low 6 bits) for j < 4, else the
+      // high nibble of W's byte j - 4 with Z's byte j - 4's top two bits (selected, not branched)
+      auto min_of = [&](int c) {
+        const int sh = 8 * ((2 * qt + c) & 3);
+        const int lo = (int)((st.h.z >> sh) & 63);
+        const int hi = (int)(((st.h.w >> (sh + 4)) & 0xF) | (((st.h.z >> (sh + 6)) & 3) << 4));
+        return qt < 2 ? lo : hi;
+      };
+      const int ma = min_of(0), mb = min_of(1);
+      const half2 mma = {(_Float16)ma, (_Float16)ma}, mmb = {(_Float16)mb, (_Float16)mb};
+      *(u32x2*)&B.b16[rb][4 * qt] = u32x2{__builtin_bit_cast(uint32_t, mma), __builtin_bit_cast(uint32_t, mmb)};
+      B.dw[rb] = d;
+      B.dm[rb] = dmin;
+      // the activation row's per-16 sums (exact fp16), block scale and 480 * sum(q8); the row's
+      // two threads are adjacent lanes
+      u32x4 v;
+      int s = 0;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int lo16 = (int16_t)(st.a16[j] & 0xffff), hi16 = (int16_t)(st.a16[j] >> 16);
+        const half2 p = {(_Float16)lo16, (_Float16)hi16};
+        v[j] = __builtin_bit_cast(uint32_t, p);
+        s += lo16 + hi16;
+      }
+      *(u32x4*)&B.a16[ra][8 * ha] = v;
+      const float fs = (float)s;               // |s| <= 128 * 128: exact
+      const float tot = fs + dpp_mov<0xB1>(fs);  // + the other half of the row (lane ^ 1), exact
+      B.dx[ra] = st.dx;
+      B.sx[ra] = (float)WOFF * tot;            // |.| <= 480 * 32768 < 2^24: exact
+    }
+  } else {
+    const float d1 = d * (float)sc0, mm1 = dmin * (float)m0;
+    const float d2 = d * (float)sc1, mm2 = dmin * (float)m1;
+    half8 lo, hi;
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+      const uint32_t byte = (st.q[t / 4] >> (8 * (t % 4))) & 0xff;
+      lo[t] = (_Float16)(d1 * (float)(byte & 0xF) - mm1);
+      hi[t] = (_Float16)(d2 * (float)(byte >> 4) - mm2);
+    }
+    *(half8*)&Bt[swb(rb, 8 * qt)] = lo;
+    *(half8*)&Bt[swb(rb, 32 + 8 * qt)] = hi;
+  }
+}
+
+// One K step of MFMAs on tiles A, Bt: wave (wm, wn) = (wid / 2, wid % 2) computes rows 64 wm ..
+// + 63, columns 64 wn .. + 63 as 2 x 2 tiles.  FRESH: the chains start here (zero accumulator
+// operand).
+template <bool FRESH>
+__device__ __forceinline__ void wide_mfma(const _Float16* A, const _Float16* Bt, floatx16 (&acc)[2][2]) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wm = wid >> 1, wn = wid & 1;
+  const int lr = lane & 31, lk = 8 * (lane >> 5);
+#pragma unroll
+  for (int kk = 0; kk < WBK; kk += 16) {
+    half8 a[2], b[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) a[i] = *(const half8*)&A[swa(64 * wm + 32 * i + lr, kk + lk)];
+#pragma unroll
+    for (int j = 0; j < 2; j++) b[j] = *(const half8*)&Bt[swb(64 * wn + 32 * j + lr, kk + lk)];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], FRESH && kk == 0 ? floatx16{} : acc[i][j], 0, 0, 0);
+  }
+}
+
+// GEMM_Q8K end of a super-block, per element in f32 as the 128 x 128 kernel's block_end:
+// isum = chain + 480 sum(q8) (one rounding), y += d_x * fma(d_w, isum, -d_min * msum), the mins
+// term msum on the matrix cores (K = 16, exact).
+__device__ __forceinline__ void wide_block_end(const WideBlock& B, const floatx16 (&acc)[2][2], floatx16 (&out)[2][2]) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wm = wid >> 1, wn = wid & 1;
+  const int lr = lane & 31, lk = 8 * (lane >> 5);
+  float dw[2], dm[2];
+  half8 bm[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int col = 64 * wn + 32 * j + lr;
+    dw[j] = B.dw[col];
+    dm[j] = B.dm[col];
+    bm[j] = *(const half8*)&B.b16[col][lk];
+  }
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int r0 = 64 * wm + 32 * i;
+    // the lane's 16 rows of tile i are 4 runs of 4 consecutive rows: one float4 each
+    float dxs[16], sxs[16];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int r = r0 + q * 8 + (lane >> 5) * 4;
+      const float4 v = *(const float4*)&B.dx[r];
+      const float4 u = *(const float4*)&B.sx[r];
+      dxs[4 * q] = v.x; dxs[4 * q + 1] = v.y; dxs[4 * q + 2] = v.z; dxs[4 * q + 3] = v.w;
+      sxs[4 * q] = u.x; sxs[4 * q + 1] = u.y; sxs[4 * q + 2] = u.z; sxs[4 * q + 3] = u.w;
+    }
+    const half8 am = *(const half8*)&B.a16[r0 + lr][lk];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const floatx16 accm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm[j], floatx16{}, 0, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const float isum = acc[i][j][e] + sxs[e];
+        const float t = fmaf(dw[j], isum, -(dm[j] * accm[e]));
+        out[i][j][e] = fmaf(dxs[e], t, out[i][j][e]);
+      }
+    }
+  }
+}
+
+// Workgroup barrier of the K loop: this wave's LDS stores complete, then s_barrier, in one asm
+// statement with a memory clobber (no memory access moves across it).  __syncthreads() would add
+// a release fence, which also waits for every LDS DMA in flight: the tiles fetched ahead.
+__device__ __forceinline__ void wide_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Vector memory operations one phase issues: 4 DMA and the weight loads of the step two ahead
+// (its qs bytes; with a super-block's first step also the header and, in GEMM_Q8K mode, the
+// activation sums and scale)
+template <int MODE, int S>
+constexpr int phase_vm() {
+  return 4 + 1 + ((S + 2) % 4 == 0 ? (MODE == GEMM_Q8K ? 3 : 1) : 0);
+}
+
+// Step p = (kb, S) of the K loop: this step's MFMAs (at S = 3 also the super-block's end), the
+// weight tile of step p + 1 from the registers loaded one phase earlier, then the activation DMA
+// of step p + 2 into its tile and the weight registers of step p + 2; the barrier follows once
+// every load issued before this phase has landed (this phase's own stay in flight).  The DMA is
+// issued after the phase's LDS stores: the compiler makes an LDS store wait for every LDS DMA in
+// flight (it cannot tell their addresses apart), which here are the previous phase's, landed by
+// then.  ia: this step's activation tile; kn: the next super-block (clamped).
+template <int MODE, int S>
+__device__ __forceinline__ void wide_phase(const GemmArgs& g, const WideOff& o, int m0, int kb, int kn, int ia,
+                                           WideSmem& s, WideStage& st, floatx16 (&acc)[2][2], floatx16 (&out)[2][2]) {
+  constexpr bool Q8 = MODE == GEMM_Q8K;
+  const int ia2 = ia == 0 ? 2 : ia - 1;  // (ia + 2) % 3
+  const int kb2 = S < 2 ? kb : kn;       // the super-block of step p + 2
+  if constexpr (Q8) wide_mfma<S == 0>(s.a[ia], s.b[S & 1], acc);
+  else wide_mfma<false>(s.a[ia], s.b[S & 1], out);
+  if constexpr (Q8 && S == 3) wide_block_end(s.blk[kb & 1], acc, out);
+  wide_store<MODE, (S + 1) % 4>(st, s.b[(S + 1) & 1], s.blk[S == 3 ? (kb + 1) & 1 : kb & 1]);
+  wide_dma_a<(S + 2) % 4>(g, o, m0, kb2, s.a[ia2]);
+  wide_load<MODE, (S + 2) % 4>(g, o, kb2, st);
+  wait_vm<phase_vm<MODE, S>()>();
+  wide_barrier();
+}
+
+template <int MODE>
+__global__ void __launch_bounds__(GT, 1) gemm_wide_kernel(const GemmArgs g) {
+  __shared__ WideSmem s;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wm = wid >> 1, wn = wid & 1;
+  // the tile's output rows / columns [m_lo, ..), [n_lo, ..); the last tiles are computed from
+  // origins shifted back so that every row and column read lies inside the matrices (M >= 256,
+  // N >= 128), and store only their own part
+  const int m_lo = blockIdx.y * WBM, n_lo = blockIdx.x * WBN;
+  const int m0 = min(m_lo, g.M - WBM), n0 = min(n_lo, g.N - WBN);
+  // split-K (small grids): split blockIdx.z of gridDim.z takes super-blocks [kb0, kb1)
+  const int nkb_all = g.K / 256, ns = gridDim.z, sz = blockIdx.z;
+  const int kb0 = sz * nkb_all / ns, nkb = (sz + 1) * nkb_all / ns;
+  const int lr = lane & 31;
+  constexpr bool Q8 = MODE == GEMM_Q8K;
+
+  floatx16 out[2][2], acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) out[i][j] = floatx16{};
+
+  // prologue: step 0 in LDS, step 1's activation DMA in flight and its weights in registers
+  const WideOff o = wide_offsets(g, m0, n0);
+  WideStage st;
+  wide_dma_a<0>(g, o, m0, kb0, s.a[0]);
+  wide_load<MODE, 0>(g, o, kb0, st);
+  wide_store<MODE, 0>(st, s.b[0], s.blk[kb0 & 1]);
+  wide_dma_a<1>(g, o, m0, kb0, s.a[1]);
+  wide_load<MODE, 1>(g, o, kb0, st);
+  wait_vm<5>();  // step 0's DMA has landed
+  __syncthreads();
+  int ia = 0;
+  auto next = [](int i) { return i == 2 ? 0 : i + 1; };
+  for (int kb = kb0; kb < nkb; kb++) {
+    // past the last block the next block is the last one again (clamped), staged into tiles and
+    // a block buffer that are not read again
+    const int kn = kb + 1 < nkb ? kb + 1 : kb;
+    wide_phase<MODE, 0>(g, o, m0, kb, kn, ia, s, st, acc, out);
+    ia = next(ia);
+    wide_phase<MODE, 1>(g, o, m0, kb, kn, ia, s, st, acc, out);
+    ia = next(ia);
+    wide_phase<MODE, 2>(g, o, m0, kb, kn, ia, s, st, acc, out);
+    ia = next(ia);
+    wide_phase<MODE, 3>(g, o, m0, kb, kn, ia, s, st, acc, out);
+    ia = next(ia);
+  }
+  wait_vm<0>();  // the DMA of the steps past the end lands before the workgroup's LDS is released
+
+  // epilogue: y[m][n] = out (+ resid[m][n]); split-K: this split's partial sums
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int n = n0 + 64 * wn + 32 * j + lr;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int m = m0 + 64 * wm + 32 * i + (e / 4) * 8 + (lane >> 5) * 4 + (e % 4);
+        if (m >= m_lo && n >= n_lo) {
+          float v = out[i][j][e];
+          if (ns > 1) {
+            g.part[((size_t)sz * g.M + m) * g.N + n] = v;
+          } else {
+            if (g.resid) v = v + g.resid[(size_t)m * g.ldr + n];
+            g.y[(size_t)m * g.ldy + n] = v;
+          }
+        }
+      }
+  }
+}
+
 // Split-K sum: y[m][n] = sum over splits s = 0, 1, .. of part[s][m][n] (+ resid[m][n])
 __global__ void __launch_bounds__(256) gemm_split_reduce_kernel(const GemmArgs g, int ns) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, mn = (size_t)g.M * g.N;
@@ -743,6 +1103,29 @@ int launch_act_prep(const ActPrepArgs& a, hipStream_t s) {
 
 int launch_gemm(const GemmArgs& g, hipStream_t s) { return launch_gemm_timed(g, s, nullptr, nullptr); }
 
+namespace {
+
+// Q4_K GEMMs of at least 256 rows and 128 columns take the 256 x 128 kernel (its last tiles are
+// shifted back inside the matrices), when every operand offset fits 32 bits; TPT_HIP_GEMM_TILE=
+// narrow forces the 128 x 128 kernel (comparisons and timing).
+bool gemm_wide(const GemmArgs& g) {
+  if (g.wtype != TPT_TYPE_Q4_K || g.M < WBM || g.N < WBN) return false;
+  if ((uint64_t)g.M * (uint64_t)g.K * 2u >= (1ull << 32) || (uint64_t)g.N * g.w_stride >= (1ull << 32)) return false;
+  const char* e = getenv("TPT_HIP_GEMM_TILE");
+  return !(e && !strcmp(e, "narrow"));
+}
+
+// Splits of K for a grid of `tiles` output tiles that cannot fill the 256 CUs: the most that
+// still run in one round (tiles x splits <= 256), at least two super-blocks per split, at most 8.
+int splits_for(int tiles, int nkb) {
+  if (tiles > 128 || nkb < 4) return 1;
+  int ns = 256 / tiles;
+  ns = std::min(ns, nkb / 2);
+  return std::min(ns, 8);
+}
+
+}  // namespace
+
 int launch_gemm_timed(const GemmArgs& g, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.K % 256) return fail(TPT_ERR_INVALID, "gemm: K must be a positive multiple of 256, M and N positive");
   const bool kq = g.wtype == TPT_TYPE_Q4_K || g.wtype == TPT_TYPE_Q5_K || g.wtype == TPT_TYPE_Q6_K;
@@ -756,6 +1139,8 @@ int launch_gemm_timed(const GemmArgs& g, hipStream_t s, hipEvent_t ev0, hipEvent
   if (!g.af) return fail(TPT_ERR_INVALID, "gemm: null activation rows");
   if ((g.mode == GEMM_Q8K && (!g.ad || (g.wtype != TPT_TYPE_Q6_K && !g.as16))) || (g.mode == GEMM_Q80 && !g.ad))
     return fail(TPT_ERR_INVALID, "gemm: quantized activations need block scales (and per-16 sums for Q4_K and Q5_K)");
+  if (((uintptr_t)g.af % 16) || ((uintptr_t)g.as16 % 16))
+    return fail(TPT_ERR_INVALID, "gemm: activation rows and per-16 sums must be 16-byte aligned");
   if (g.w_stride < row_bytes(g.wtype, g.K))
     return fail(TPT_ERR_INVALID, "gemm: weight row stride shorter than a row");
   const bool a16 = g.wtype == TPT_TYPE_Q4_K || g.wtype == TPT_TYPE_Q5_K || g.wtype == TPT_TYPE_F16;
@@ -763,11 +1148,17 @@ int launch_gemm_timed(const GemmArgs& g, hipStream_t s, hipEvent_t ev0, hipEvent
     return fail(TPT_ERR_INVALID, "gemm: Q4_K, Q5_K and F16 weight rows must be 16-byte aligned");
   if (!a16 && ((g.w_stride % 2) || ((uintptr_t)g.w % 2)))
     return fail(TPT_ERR_INVALID, "gemm: Q6_K, Q8_0 and Q4_0 weight rows must be 2-byte aligned");
-  int ns = gemm_splits(g.M, g.N, g.K);
+  const bool wide = gemm_wide(g);
+  const int tm = wide ? WBM : BM;
+  const int tiles = ((g.N + BN - 1) / BN) * ((g.M + tm - 1) / tm);
+  int ns = splits_for(tiles, g.K / 256);
   if (!g.part || g.part_floats < (size_t)ns * g.M * g.N) ns = 1;  // no workspace: one pass over K
-  const dim3 grid((unsigned)((g.N + BN - 1) / BN), (unsigned)((g.M + BM - 1) / BM), (unsigned)ns);
+  const dim3 grid((unsigned)((g.N + BN - 1) / BN), (unsigned)((g.M + tm - 1) / tm), (unsigned)ns);
   hipEvent_t e1 = ns > 1 ? nullptr : ev1;  // split-K: the stop event goes on the sum kernel
-  if (g.wtype == TPT_TYPE_Q4_K) {
+  if (wide) {
+    if (g.mode == GEMM_Q8K) hipExtLaunchKernelGGL((gemm_wide_kernel<GEMM_Q8K>), grid, dim3(GT), 0, s, ev0, e1, 0, g);
+    else hipExtLaunchKernelGGL((gemm_wide_kernel<GEMM_F16>), grid, dim3(GT), 0, s, ev0, e1, 0, g);
+  } else if (g.wtype == TPT_TYPE_Q4_K) {
     if (g.mode == GEMM_Q8K) hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q4_K, GEMM_Q8K>), grid, dim3(GT), 0, s, ev0, e1, 0, g);
     else hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q4_K, GEMM_F16>), grid, dim3(GT), 0, s, ev0, e1, 0, g);
   } else if (g.wtype == TPT_TYPE_Q5_K) {
@@ -793,15 +1184,11 @@ int launch_gemm_timed(const GemmArgs& g, hipStream_t s, hipEvent_t ev0, hipEvent
   return TPT_OK;
 }
 
-// Splits of K for an M x N x K GEMM whose output has fewer tiles than the 256 CUs: the most
-// that still run in one round (tiles x splits <= 256), at least two super-blocks per split, at
-// most 8.
+// Split-K workspace bound for an M x N x K GEMM: the larger split count of the two tile shapes
+// (the launch uses the count of the kernel it picks).
 int gemm_splits(int M, int N, int K) {
-  const int tiles = ((N + BN - 1) / BN) * ((M + BM - 1) / BM), nkb = K / 256;
-  if (tiles > 128 || nkb < 4) return 1;
-  int ns = 256 / tiles;
-  ns = std::min(ns, nkb / 2);
-  return std::min(ns, 8);
+  const int cols = (N + BN - 1) / BN, nkb = K / 256;
+  return std::max(splits_for(cols * ((M + BM - 1) / BM), nkb), splits_for(cols * ((M + WBM - 1) / WBM), nkb));
 }
 
 }  // namespace tpt
