@@ -649,14 +649,17 @@ __global__ void __launch_bounds__(GT, 1) gemm_kernel(const GemmArgs g) {
 // that kernel's, so both produce the same bits.
 constexpr int WBM = 256, WBN = 128, WBK = 64;
 constexpr int WOFF = 480;  // a multiple of 32: 1024 sc + WOFF is exact in fp16 up to sc = 63
-// Rows of 64 fp16 (128 bytes): the 16-byte chunk c of row r sits at c ^ f(r % 8) with f a
-// permutation, so the 8 rows one MFMA operand read covers per chunk column hit 8 distinct chunk
-// positions.  A rows: f = identity (each staging thread writes 4 chunks of one half of a row).
-// B rows: f(r) = 4 (r % 2) + (r / 2) % 4, so that the two rows one 8-lane store group covers (4
-// threads per row, one chunk each in a half of the row) land in opposite halves.
-__device__ __forceinline__ int swa(int r, int k) { return r * WBK + (((k >> 3) ^ (r & 7)) << 3); }
+// Rows of 64 fp16 (128 bytes, half of gfx950's 64 LDS banks): the 16-byte chunk c of row r sits
+// at c ^ f((r / 2) % 8), f a permutation.  One 16-lane group of an MFMA operand read covers rows
+// r0 .. r0 + 15 at one chunk column: the even rows fill one half of the banks, the odd rows the
+// other, and within each half f gives the 8 rows 8 distinct chunk positions.  A rows: f =
+// identity (written by DMA, whole 1 KB runs).  B rows: f(x) = 4 (x % 2) + x / 2, so that the two
+// rows of equal parity in one 16-lane store group (4 rows, 4 threads each writing one chunk of
+// the same half of a row) land in opposite halves of the chunk positions.
+__device__ __forceinline__ int swa(int r, int k) { return r * WBK + (((k >> 3) ^ ((r >> 1) & 7)) << 3); }
 __device__ __forceinline__ int swb(int r, int k) {
-  return r * WBK + (((k >> 3) ^ (((r & 1) << 2) | ((r >> 1) & 3))) << 3);
+  const int x = (r >> 1) & 7;
+  return r * WBK + (((k >> 3) ^ (((x & 1) << 2) | (x >> 1))) << 3);
 }
 struct WideBlock {               // GEMM_Q8K: one super-block's per-row and per-column data
   _Float16 a16[WBM][LDG];        // activation per-16 sums
@@ -685,18 +688,20 @@ struct WideStage {
 };
 // A thread's byte offsets from the operand bases, fixed over the K loop (32-bit: the launcher
 // keeps every operand below 4 GiB, so loads take a uniform base plus one offset register): its
-// DMA lanes' offset within a group of 8 activation rows (row l / 8, chunk (l % 8) ^ (l / 8)),
-// its weight row, its activation row's per-16 sums and block scales.  The tile's rows and
-// columns all lie inside the matrices (the last tiles are shifted back, see gemm_wide_kernel),
-// so no index is clamped.
+// DMA lane's offset within a group of 8 activation rows (row l / 8 and the chunk that position
+// l % 8 holds, for groups of even (a0) and odd (a1) index), its weight row, its activation row's
+// per-16 sums and block scales.  The tile's rows and columns all lie inside the matrices (the
+// last tiles are shifted back, see gemm_wide_kernel), so no index is clamped.
 struct WideOff {
-  uint32_t a, w, s16, sd;
+  uint32_t a0, a1, w, s16, sd;
 };
 __device__ __forceinline__ WideOff wide_offsets(const GemmArgs& g, int m0, int n0) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int p = lane & 7, rr = lane >> 3;
   WideOff o;
-  o.a = (uint32_t)rr * (uint32_t)g.K * 2u + 16u * (uint32_t)(p ^ rr);
+  // row 8 k + rr of the tile: (row / 2) % 8 = 4 (k % 2) + rr / 2
+  o.a0 = (uint32_t)rr * (uint32_t)g.K * 2u + 16u * (uint32_t)(p ^ (rr >> 1));
+  o.a1 = (uint32_t)rr * (uint32_t)g.K * 2u + 16u * (uint32_t)(p ^ ((rr >> 1) + 4));
   const uint32_t m = (uint32_t)(m0 + (tid >> 1)), n = (uint32_t)(n0 + (tid >> 2));
   o.w = n * (uint32_t)g.w_stride;
   o.s16 = m * (uint32_t)(g.K / 16) * 2u + 16u * (uint32_t)(tid & 1);
@@ -718,7 +723,7 @@ __device__ __forceinline__ void wide_load(const GemmArgs& g, const WideOff& o, i
 // The activation tile of step S of super-block kb, by LDS DMA (global_load_lds_dwordx4: lane l of
 // a wave writes the 16 bytes at LDS offset 16 l of the instruction's 1 KB): wave w's instruction i
 // fills rows 8 (4 w + i) .. + 7, lane l position l % 8 of row 8 (4 w + i) + l / 8, which holds
-// that row's chunk (l % 8) ^ (l / 8).  Complete once the wave's vector memory count drains.
+// the chunk swa places there.  Complete once the wave's vector memory count drains.
 template <int S>
 __device__ __forceinline__ void wide_dma_a(const GemmArgs& g, const WideOff& o, int m0, int kb, _Float16* A) {
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar bases
@@ -726,7 +731,7 @@ __device__ __forceinline__ void wide_dma_a(const GemmArgs& g, const WideOff& o, 
   for (int i = 0; i < 4; i++) {
     const uint32_t r0 = (uint32_t)(m0 + 8 * (4 * w + i));  // the instruction's first row
     const char* base = (const char*)g.af + (r0 * (uint32_t)g.K * 2u + (uint32_t)kb * 512u + 2u * WBK * S);
-    __builtin_amdgcn_global_load_lds(base + o.a, (__attribute__((address_space(3))) void*)&A[8 * WBK * (4 * w + i)], 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(base + (i & 1 ? o.a1 : o.a0), (__attribute__((address_space(3))) void*)&A[8 * WBK * (4 * w + i)], 16, 0, 0);
   }
 }
 
