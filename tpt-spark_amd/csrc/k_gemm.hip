@@ -939,7 +939,6 @@ __global__ void __launch_bounds__(GT, 1) gemm_wide_kernel(const GemmArgs g) {
   const int nkb_all = g.K / 256, ns = gridDim.z, sz = blockIdx.z;
   const int kb0 = sz * nkb_all / ns, nkb = (sz + 1) * nkb_all / ns;
   const int lr = lane & 31;
-  constexpr bool Q8 = MODE == GEMM_Q8K;
 
   floatx16 out[2][2], acc[2][2];
 #pragma unroll

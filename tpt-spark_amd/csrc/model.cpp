@@ -263,6 +263,7 @@ int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_t
     L.tq = t.q->type; L.tk = t.k->type; L.tv = t.v->type; L.to = t.o->type;
     L.tg = t.g->type; L.tu = t.u->type; L.td = t.d->type;
     L.qkv_adjacent = L.tq == L.tk && L.tk == L.tv && L.k == L.q + t.q->bytes && L.v == L.k + t.k->bytes;
+    L.gu_adjacent = L.tg == L.tu && L.up == L.gate + t.g->bytes;
   }
   embd = dev(te);
   embd_type = te->type;
@@ -658,12 +659,12 @@ int tpt_model::prefill_scratch(int T, int n_chunks) {
                o_af2 = carve(has_f16_matrix ? (size_t)T * Kmax * 2 : 0),
                o_ad = carve((size_t)T * (Kmax / 32) * 4), o_as = carve((size_t)T * (Kmax / 16) * 2),
                o_qkv = carve((size_t)T * (qd + 2 * kd) * 4), o_q = carve((size_t)T * qd * 4),
-               o_att = carve((size_t)T * qd * 4), o_g = carve((size_t)T * F * 4), o_u = carve((size_t)T * F * 4),
+               o_att = carve((size_t)T * qd * 4), o_g = carve((size_t)T * 2 * F * 4),
                o_part = carve((size_t)T * attn_part_floats(desc.n_heads, desc.n_kv_heads, desc.head_dim, n_chunks) * 4),
                o_ids = carve((size_t)T * 4);
   // split-K workspace of the GEMMs (short prompts): the largest splits x T x N over the shapes
   size_t gsplit = 0;
-  const int shapes[4][2] = {{H, qd + 2 * kd}, {qd, H}, {H, F}, {F, H}};  // (K, N)
+  const int shapes[5][2] = {{H, qd + 2 * kd}, {qd, H}, {H, F}, {H, 2 * F}, {F, H}};  // (K, N)
   for (const auto& kn : shapes) {
     const int ns = gemm_splits(T, kn[1], kn[0]);
     if (ns > 1) gsplit = std::max(gsplit, (size_t)ns * T * kn[1]);
@@ -688,8 +689,8 @@ int tpt_model::prefill_scratch(int T, int n_chunks) {
   pf_qkv = (float*)(b + o_qkv);
   pf_q = (float*)(b + o_q);
   pf_att = (float*)(b + o_att);
-  pf_g = (float*)(b + o_g);
-  pf_u = (float*)(b + o_u);
+  pf_g = (float*)(b + o_g);  // rows of 2F: gate outputs, then up outputs
+  pf_u = pf_g + F;
   pf_part = (float*)(b + o_part);
   pf_ids = (uint32_t*)(b + o_ids);
   pf_gsplit = gsplit ? (float*)(b + o_gsplit) : nullptr;
@@ -735,11 +736,11 @@ int tpt_model::batched_layers(int T, int p0, int l0, int l1) {
   // activation rows of (x, x2, norm) in the mode the next GEMM needs; rows already prepared
   // for the same input and mode are reused
   struct Prepared { const float* x; const float* x2; const float* nw; int K, mode; } last{nullptr, nullptr, nullptr, 0, -1};
-  auto prep = [&](const float* xx, const float* x2, int K, const float* nw, int type) {
+  auto prep = [&](const float* xx, const float* x2, int K, const float* nw, int type, int ldx = 0) {
     const int mode = mode_of(type);
     if (last.x == xx && last.x2 == x2 && last.nw == nw && last.K == K && last.mode == mode) return (int)TPT_OK;
     ActPrepArgs a;
-    a.M = T; a.K = K; a.ldx = K; a.x = xx; a.x2 = x2; a.norm_w = nw; a.eps = desc.rms_eps;
+    a.M = T; a.K = K; a.ldx = ldx ? ldx : K; a.x = xx; a.x2 = x2; a.norm_w = nw; a.eps = desc.rms_eps;
     a.mode = mode; a.af = pf_af; a.ad = pf_ad; a.as16 = pf_as16;
     a.af2 = mode == GEMM_F16 ? pf_af2 : nullptr;
     last = {xx, x2, nw, K, mode};
@@ -789,10 +790,17 @@ int tpt_model::batched_layers(int T, int p0, int l0, int l1) {
     if ((rc = prep(pf_att, nullptr, qd, nullptr, L.to)) || (rc = gemm(L.to, L.o, qd, H, pf_x, H, pf_x))) return rc;
     // pf_x changed in place: the rows prepared from it before are stale
     last.mode = -1;
-    if ((rc = prep(pf_x, nullptr, H, L.ffn_norm, L.tg)) || (rc = gemm(L.tg, L.gate, H, F, pf_g, F, nullptr)) ||
-        (rc = prep(pf_x, nullptr, H, L.ffn_norm, L.tu)) || (rc = gemm(L.tu, L.up, H, F, pf_u, F, nullptr)))
-      return rc;
-    if ((rc = prep(pf_g, pf_u, F, nullptr, L.td)) || (rc = gemm(L.td, L.down, F, H, pf_x, H, pf_x))) return rc;
+    // gate and up outputs side by side in rows of 2F; adjacent matrices of one type are one GEMM
+    // over 2F weight rows (twice the output tiles: whole rounds over the CUs at 2048 positions)
+    if (L.gu_adjacent) {
+      if ((rc = prep(pf_x, nullptr, H, L.ffn_norm, L.tg)) || (rc = gemm(L.tg, L.gate, H, 2 * F, pf_g, 2 * F, nullptr)))
+        return rc;
+    } else {
+      if ((rc = prep(pf_x, nullptr, H, L.ffn_norm, L.tg)) || (rc = gemm(L.tg, L.gate, H, F, pf_g, 2 * F, nullptr)) ||
+          (rc = prep(pf_x, nullptr, H, L.ffn_norm, L.tu)) || (rc = gemm(L.tu, L.up, H, F, pf_u, 2 * F, nullptr)))
+        return rc;
+    }
+    if ((rc = prep(pf_g, pf_u, F, nullptr, L.td, 2 * F)) || (rc = gemm(L.td, L.down, F, H, pf_x, H, pf_x))) return rc;
     last.mode = -1;
   }
   return TPT_OK;

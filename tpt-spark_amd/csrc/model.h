@@ -15,6 +15,7 @@ struct tpt_model {
     const float *attn_norm = nullptr, *ffn_norm = nullptr;
     int tq = 0, tk = 0, tv = 0, to = 0, tg = 0, tu = 0, td = 0;
     bool qkv_adjacent = false;  // q, k, v rows contiguous in HBM and of one type
+    bool gu_adjacent = false;   // gate and up rows contiguous in HBM and of one type
   };
 
   tpt_ctx* ctx = nullptr;  // not owned
