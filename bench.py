@@ -163,7 +163,10 @@ def attn_causal_roofline(tp, ctx, iters=20):
 
 
 # prefill GEMM shapes: M prompt rows, K = 4096, N = 4096 (Q/O) and 14336 (gate/up)
-GEMM_CASES = [(M, 4096, N) for M in (128, 512, 2048) for N in (4096, 14336)]
+# prompt shapes at K=4096, then the 8B model's other prefill GEMMs over a 2048-position slice:
+# Q|K|V (N=6144), gate|up as one GEMM (N=28672) and down (K=14336)
+GEMM_CASES = [(M, 4096, N) for M in (128, 512, 2048) for N in (4096, 14336)] + \
+             [(2048, 4096, 6144), (2048, 4096, 28672), (2048, 14336, 4096)]
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
 
