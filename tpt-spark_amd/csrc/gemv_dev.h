@@ -599,7 +599,9 @@ struct NoHook {
 
 // One workgroup's share of a GEMV: rows [wg * rows_per_wg, ...).  WT weight type; BPP
 // super-blocks per row per pass (16, or fewer for short rows, then RPP = 16/BPP rows share a
-// pass); RB row slots per step; NMAT matrices (2: gate|up); KS-way split of the passes across
+// pass); RB row slots per step; NMAT matrices (2: gate|up, streamed one after the other: the
+// workgroup's gate rows, then its up rows, as 2 rows_per_wg rows of one walk, so that at any
+// step the waves read one contiguous window); KS-way split of the passes across
 // waves; D steps in flight per wave; NORM: RMSNorm prologue; ONEPASS: one pass per row (the
 // lane's activation slice is then the same at every step and is read from LDS once).  hook()
 // runs after the activation and the first weight loads are issued, before the activation is
@@ -633,10 +635,12 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int 
   const Lds L = lds_layout(smem, K, act_kind<WT>());
   const int RPW = geo.rows_per_wg;
   const int r0 = wg * RPW;
+  constexpr bool PAIR = NMAT == 2;
+  const int VR = PAIR ? 2 * RPW : RPW;  // rows of the walk: gate rows, then up rows
   const int rp = lane / LPR, sb = (lane / 4) % BPP, q = lane & 3;
 
   // this wave's row groups and passes
-  const int ngrp = RPW / RG;
+  const int ngrp = VR / RG;
   const int wr = wid / KS, ks = wid % KS;
   // row groups wr, wr + WR, ...: at any step the waves of a k-split read adjacent rows, so a
   // workgroup streams one contiguous window of the matrix
@@ -648,13 +652,13 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int 
 
   // 2. weight steps in a ring of D register slots (slot d holds steps d, d + D, ...), the first
   //    D issued before the prologue
-  Raw<WT> ring[D][RB][NMAT];
+  Raw<WT> ring[D][RB];
   auto group_of = [&](int p, bool* valid) {  // this lane's weight group in pass p
     const int blk = p * BPP + sb;
     *valid = blk < nb;
     return 4 * (blk < nb ? blk : nb - 1) + q;
   };
-  auto issue = [&](Raw<WT> (&buf)[RB][NMAT], int s) {
+  auto issue = [&](Raw<WT> (&buf)[RB], int s) {
     if (s >= S) s = S > 0 ? S - 1 : 0;  // past the end: re-read the last step (cache hits)
     const int pp = PP > 0 ? PP : 1;
     const int grp = wr + (s / pp) * WR, p = pa + s % pp;
@@ -662,11 +666,11 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int 
     const int g = group_of(p, &v);
 #pragma unroll
     for (int j = 0; j < RB; j++) {
-      int row = r0 + (grp * RB + j) * RPP + rp;
+      const int vr = (grp * RB + j) * RPP + rp;
+      const bool up = PAIR && vr >= RPW;
+      int row = r0 + (up ? vr - RPW : vr);
       if (row >= N) row = N - 1;
-#pragma unroll
-      for (int m = 0; m < NMAT; m++)
-        load_raw<WT>((m == 0 ? A.w0 : A.w1) + (size_t)row * A.row_stride, g, buf[j][m]);
+      load_raw<WT>((up ? A.w1 : A.w0) + (size_t)row * A.row_stride, g, buf[j]);
     }
   };
   // 0. the epilogue's own operands (residual, step position, argmax slot) are read before
@@ -707,39 +711,33 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int 
     }
   }
 
-  float acc[RB][NMAT];
+  float acc[RB];
 #pragma unroll
-  for (int j = 0; j < RB; j++)
-#pragma unroll
-    for (int m = 0; m < NMAT; m++) acc[j][m] = 0.f;
+  for (int j = 0; j < RB; j++) acc[j] = 0.f;
 
   using ActT = typename ActOf<WT>::T;
-  auto compute = [&](const Raw<WT> (&buf)[RB][NMAT], int s, const ActT& act, int g, bool v) {
+  auto compute = [&](const Raw<WT> (&buf)[RB], int s, const ActT& act, int g, bool v) {
     const int grp = wr + (s / PP) * WR, p = pa + s % PP;
 #pragma unroll
-    for (int j = 0; j < RB; j++)
-#pragma unroll
-      for (int m = 0; m < NMAT; m++) {
-        const float t = dot_group(buf[j][m], act, g);
-        acc[j][m] += v ? t : 0.f;
-      }
+    for (int j = 0; j < RB; j++) {
+      const float t = dot_group(buf[j], act, g);
+      acc[j] += v ? t : 0.f;
+    }
     if (p == pb - 1) {  // row group done: the row's partial sums to LDS
 #pragma unroll
-      for (int j = 0; j < RB; j++)
-#pragma unroll
-        for (int m = 0; m < NMAT; m++) {
-          float t;
-          int part = 0;
-          if constexpr (LPR >= 16) {
-            t = sum16(acc[j][m]);
-            part = (lane % LPR) >> 4;
-          } else {
-            t = lane_group_sum<LPR>(acc[j][m]);
-          }
-          if (lane % (LPR >= 16 ? 16 : LPR) == 0)
-            L.rows[(((size_t)ks * RPW + (grp * RB + j) * RPP + rp) * NMAT + m) * NPART + part] = t;
-          acc[j][m] = 0.f;
+      for (int j = 0; j < RB; j++) {
+        float t;
+        int part = 0;
+        if constexpr (LPR >= 16) {
+          t = sum16(acc[j]);
+          part = (lane % LPR) >> 4;
+        } else {
+          t = lane_group_sum<LPR>(acc[j]);
         }
+        if (lane % (LPR >= 16 ? 16 : LPR) == 0)
+          L.rows[((size_t)ks * VR + (grp * RB + j) * RPP + rp) * NPART + part] = t;
+        acc[j] = 0.f;
+      }
     }
   };
 
@@ -779,7 +777,7 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int 
   auto row_val = [&](int i, int m) {
     float t = 0.f;
 #pragma unroll
-    for (int k = 0; k < KS; k++) t += row_total<NPART>(L.rows + (((size_t)k * RPW + i) * NMAT + m) * NPART);
+    for (int k = 0; k < KS; k++) t += row_total<NPART>(L.rows + ((size_t)k * VR + i + m * RPW) * NPART);
     return t;
   };
   switch (A.epilogue) {
