@@ -233,13 +233,10 @@ int tpt_model_decode_greedy(tpt_model* m, uint32_t first, int pos0, int n_steps,
 int tpt_model_hidden(tpt_model* m, float* out_host);
 /* How a decode step runs on the device.  Replaces the per-token loop of
  * WgpuEngine::run_forward_pass (src-tauri/src/engine/wgpu_engine.rs:339-490), which submits
- * each op of each layer separately.  TPT_DECODE_KERNELS: one launch per fused op (6 per
- * layer), captured into a HIP graph per step.  TPT_DECODE_PERSISTENT: the embedding and every
- * layer in one launch of one workgroup per compute unit, with grid barriers between the
- * phases, then the LM head launch; available where the model's shape has such a kernel (every
- * layer matrix Q4_K; TPT_ERR_UNSUPPORTED otherwise).  The default is TPT_DECODE_KERNELS (the
- * environment variable TPT_HIP_DECODE=persistent selects the other at load).  Both paths run
- * the same arithmetic in the same order: their logits and tokens are bit-identical. */
+ * each op of each layer separately.  TPT_DECODE_KERNELS (the only form): one launch per fused
+ * op, captured into a HIP graph per step.  TPT_DECODE_PERSISTENT (one launch for every layer,
+ * grid barriers between the phases) was measured slower and removed: setting it returns
+ * TPT_ERR_UNSUPPORTED; the value stays reserved. */
 #define TPT_DECODE_KERNELS 0
 #define TPT_DECODE_PERSISTENT 1
 int tpt_model_set_decode_path(tpt_model* m, int path);

@@ -561,11 +561,39 @@ int orc_gemv_f64(int type, int64_t k, int64_t n, const void* w, const double* x,
 
 /* ------------------------------------------------------------------ small ops */
 
+/* Summation-order variant of rms_norm's sum of squares (test instrument, off by default): fused
+ * multiply-add sums over runs of 16 elements, then the run sums added pairwise as a tree -- the
+ * shape of a GPU reduction.  Same squares, different f32 rounding. */
+static int g_rms_order = 0;
+
+void orc_set_rms_order(int on) { g_rms_order = on != 0; }
+
+static float sum_squares_tree(const float* x, int64_t n) {
+  const int64_t m0 = n / 16;
+  float* p = (float*)malloc(sizeof(float) * (size_t)m0);
+  for (int64_t j = 0; j < m0; j++) {
+    float s = 0.f;
+    for (int i = 0; i < 16; i++) s = fmaf(x[16 * j + i], x[16 * j + i], s);
+    p[j] = s;
+  }
+  int64_t m = m0;
+  while (m > 1) {
+    for (int64_t i = 0; i < m / 2; i++) p[i] = p[2 * i] + p[2 * i + 1];
+    if (m & 1) p[m / 2] = p[m - 1];
+    m = (m + 1) / 2;
+  }
+  const float t = p[0];
+  free(p);
+  return t;
+}
+
 /* candle_nn::ops::rms_norm CPU: sum2 sequential in f32, m = sqrt(sum2/dim + eps),
  * y = x / m * alpha */
 void orc_rmsnorm(const float* x, const float* w, int64_t n, float eps, float* y) {
   float sum2 = 0.f;
-  for (int64_t i = 0; i < n; i++) sum2 += x[i] * x[i];
+  if (g_rms_order && n >= 16 && n % 16 == 0) sum2 = sum_squares_tree(x, n);
+  else
+    for (int64_t i = 0; i < n; i++) sum2 += x[i] * x[i];
   const float m = sqrtf(sum2 / (float)n + eps);
   for (int64_t i = 0; i < n; i++) y[i] = x[i] / m * w[i];
 }

@@ -129,6 +129,8 @@ int orc_model_run_layers(orc_model* m, const float* x_in, int n, int pos0, int l
  * instrument: the same integers with another f32 rounding, to measure how far a model's
  * outputs move under a change of summation order alone. */
 void orc_set_dot_block_order(int on);
+/* test instrument: RMSNorm's sum of squares in a 16-run + pairwise-tree order (off: candle's) */
+void orc_set_rms_order(int on);
 /* copy of one layer's K and V cache, each [n_kv_heads][max_pos][head_dim] f32 */
 int orc_model_kv(const orc_model* m, int layer, float* k_out, float* v_out);
 int orc_model_last_hidden(const orc_model* m, float* out);

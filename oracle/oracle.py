@@ -58,6 +58,7 @@ def lib():
         L.orc_model_kv.argtypes = [P, I32, P, P]
         L.orc_model_run_layers.argtypes = [P, P, I32, I32, I32, I32, P, I32]
         L.orc_set_dot_block_order.argtypes = [I32]
+        L.orc_set_rms_order.argtypes = [I32]
         L.orc_model_prime_cache.argtypes = [P, I32, C.c_uint64]
         L.orc_model_tensor.argtypes = [P, C.c_char_p, P, P, P]
         L.orc_model_tensor.restype = P
@@ -158,6 +159,12 @@ def attention(q, kc, vc, nq, nkv, hd, L):
 def set_dot_block_order(on):
     """k-quant dot products in the block-reduced f32 order (a test instrument; off = candle's)."""
     lib().orc_set_dot_block_order(int(on))
+
+
+def set_rms_order(on):
+    """RMSNorm's sum of squares in a 16-run + pairwise-tree order (a test instrument; off =
+    candle's sequential sum)."""
+    lib().orc_set_rms_order(int(on))
 
 
 def argmax(logits):

@@ -31,11 +31,12 @@ def gguf_8b(tmp_path_factory):
     os.remove(path)
 
 
-def _forced(path, prompt, toks, fma=True, block_order=False):
+def _forced(path, prompt, toks, fma=True, block_order=False, rms_order=False):
     om = oracle.Model(path)
     try:
         om.set_attn_fma(fma)
         oracle.set_dot_block_order(block_order)
+        oracle.set_rms_order(rms_order)
         om.reset(len(prompt) + len(toks) + 1, kv_f16=False)
         out = [om.forward(prompt, 0, NT)]
         for i, t in enumerate(toks[:-1]):
@@ -43,6 +44,7 @@ def _forced(path, prompt, toks, fma=True, block_order=False):
         return np.stack(out)
     finally:
         oracle.set_dot_block_order(False)
+        oracle.set_rms_order(False)
         om.close()
 
 
@@ -55,9 +57,14 @@ def _margin(l):
 def test_8b_teacher_forced_short(ctx, gguf_8b):
     """16 prompt tokens then the oracle's 8 greedy tokens, teacher-forced, f32 cache (candle's).
     Bar as at the 1B shape: S = the largest max-abs logit distance between the oracle and the
-    oracle under the other plausible candle summation orders (attention without FMA; block-
-    reduced k-quant dots); every step within S, and the same greedy token wherever the oracle's
-    top-two margin exceeds S."""
+    oracle under the other plausible summation orders (attention without FMA; block-reduced
+    k-quant dots; RMSNorm's sum of squares in a tree order; all three at once, as the device
+    changes every reduction's order together).  With 8 steps, S is the largest of 32 equally
+    likely deviations and a device that differs only in rounding order would exceed it about
+    one run in five, so the bar carries a margin of 1.5: every step within 1.5 S in max-abs and
+    within 1.5 times the probes' largest relative L2 (a composition error, a misplaced norm or
+    residual, moves relative L2 to ~1 against ~0.1 here), and the same greedy token wherever the
+    oracle's top-two margin exceeds 1.5 S."""
     prompt = [int(t) for t in np.random.default_rng(SEED).integers(0, 128256, 16)]
     om = oracle.Model(gguf_8b)
     try:
@@ -65,9 +72,13 @@ def test_8b_teacher_forced_short(ctx, gguf_8b):
     finally:
         om.close()
     ref = _forced(gguf_8b, prompt, toks)
-    spread = np.maximum(np.abs(_forced(gguf_8b, prompt, toks, fma=False) - ref).max(axis=1),
-                        np.abs(_forced(gguf_8b, prompt, toks, block_order=True) - ref).max(axis=1))
-    S = float(spread.max())
+    alts = [_forced(gguf_8b, prompt, toks, fma=False), _forced(gguf_8b, prompt, toks, block_order=True),
+            _forced(gguf_8b, prompt, toks, rms_order=True),
+            _forced(gguf_8b, prompt, toks, fma=False, block_order=True, rms_order=True)]
+    spread = np.max([np.abs(a - ref).max(axis=1) for a in alts], axis=0)
+    S = 1.5 * float(spread.max())
+    Rl = 1.5 * max(float((np.linalg.norm(a - ref, axis=1) / np.linalg.norm(ref, axis=1)).max())
+                   for a in alts)
     m = tpthip.Model(ctx, gguf_8b, max_ctx=64, kv_type=tpthip.TYPE_F32)
     try:
         nxt, lg = m.prefill(prompt, 0, logits=True)
@@ -84,7 +95,9 @@ def test_8b_teacher_forced_short(ctx, gguf_8b):
     print(f"8B teacher-forced: gpu-oracle rel-l2 per step {np.round(rel, 4).tolist()}")
     print(f"8B teacher-forced: gpu-oracle max-abs per step {np.round(dev, 4).tolist()}; oracle "
           f"spread per step {np.round(spread, 4).tolist()}; margins {np.round(margins, 3).tolist()}")
+    print(f"8B teacher-forced: bars 1.5 S {S:.4f}, 1.5 R {Rl:.4f}")
     assert dev.max() <= S, (dev.max(), S)
+    assert rel.max() <= Rl, (rel.max(), Rl)
     for i in range(len(toks)):
         if margins[i] > S:
             assert gtok[i] == toks[i], i
@@ -164,12 +177,6 @@ def test_8b_full_size_properties(ctx, gguf_8b):
             runs.append((first, toks, last))
         assert runs[0][0] == runs[1][0] and runs[0][1] == runs[1][1] and len(runs[0][1]) == 256
         assert np.array_equal(runs[0][2], runs[1][2])
-        try:
-            m.decode_path = m.DECODE_PERSISTENT
-        except tpthip.TptError:
-            return  # no persistent kernel for this shape
-        first = m.prefill(prompt, 0)
-        assert m.decode_greedy(first, len(prompt), 256) == runs[0][1]
     finally:
         m.close()
         ms.close()

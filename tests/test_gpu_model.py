@@ -593,20 +593,23 @@ def test_1b_layers_teacher_forced(ctx, gguf_1b, kv):
 _FORCED = {}
 
 
-def _forced_logits(path, prompt, toks, fma=True, block_order=False, nthreads=16, kv_f16=False):
+def _forced_logits(path, prompt, toks, fma=True, block_order=False, nthreads=16, kv_f16=False,
+                   rms_order=False):
     """Oracle logits at every step of a teacher-forced run (f32 cache, candle's, unless kv_f16):
     step 0 after the prompt, step i after feeding toks[i-1].  Cached per arguments."""
-    key = (path, tuple(prompt), tuple(toks), fma, block_order, kv_f16)
+    key = (path, tuple(prompt), tuple(toks), fma, block_order, kv_f16, rms_order)
     if key not in _FORCED:
-        _FORCED[key] = _forced_logits_run(path, prompt, toks, fma, block_order, nthreads, kv_f16)
+        _FORCED[key] = _forced_logits_run(path, prompt, toks, fma, block_order, nthreads, kv_f16,
+                                          rms_order)
     return _FORCED[key]
 
 
-def _forced_logits_run(path, prompt, toks, fma, block_order, nthreads, kv_f16):
+def _forced_logits_run(path, prompt, toks, fma, block_order, nthreads, kv_f16, rms_order=False):
     om = oracle.Model(path)
     try:
         om.set_attn_fma(fma)
         oracle.set_dot_block_order(block_order)
+        oracle.set_rms_order(rms_order)
         om.reset(len(prompt) + len(toks) + 1, kv_f16=kv_f16)
         out = [om.forward(prompt, 0, nthreads)]
         for i, t in enumerate(toks[:-1]):
@@ -614,6 +617,7 @@ def _forced_logits_run(path, prompt, toks, fma, block_order, nthreads, kv_f16):
         return np.stack(out)
     finally:
         oracle.set_dot_block_order(False)
+        oracle.set_rms_order(False)
         om.close()
 
 
@@ -659,8 +663,10 @@ def test_1b_teacher_forced_decode(ctx, gguf_1b):
     and this random-init model amplifies any order change (a Q8_K activation value that rounds
     the other way moves the next layer), so the bar is the oracle's own spread S: the largest
     max-abs logit distance, over all 128 steps, between the oracle and the oracle run with the
-    other two plausible candle orders (separate multiply-adds in attention, as the gemm crate on a
-    host without FMA; block-reduced k-quant dot products).  Every step: GPU logits within S of
+    other plausible orders (separate multiply-adds in attention, as the gemm crate on a host
+    without FMA; block-reduced k-quant dot products; RMSNorm's sum of squares in the tree order
+    a GPU reduction takes; all three at once, as the device changes every reduction's order
+    together).  Every step: GPU logits within S of
     the oracle, and the GPU's greedy token equal to the oracle's wherever the oracle's top-two
     margin exceeds S (a margin below S is a token candle itself could pick either way).  Then
     free-running: the GPU's greedy tokens equal the oracle's up to the first such close step, and
@@ -670,7 +676,10 @@ def test_1b_teacher_forced_decode(ctx, gguf_1b):
     ref = _forced_logits(gguf_1b, PROMPT_1B, ref_toks, nthreads=nt)
     alt_fma = _forced_logits(gguf_1b, PROMPT_1B, ref_toks, fma=False, nthreads=nt)
     alt_blk = _forced_logits(gguf_1b, PROMPT_1B, ref_toks, block_order=True, nthreads=nt)
-    spread = np.maximum(np.abs(alt_fma - ref).max(axis=1), np.abs(alt_blk - ref).max(axis=1))
+    alt_rms = _forced_logits(gguf_1b, PROMPT_1B, ref_toks, rms_order=True, nthreads=nt)
+    alt_all = _forced_logits(gguf_1b, PROMPT_1B, ref_toks, fma=False, block_order=True, rms_order=True,
+                             nthreads=nt)
+    spread = np.max([np.abs(a - ref).max(axis=1) for a in (alt_fma, alt_blk, alt_rms, alt_all)], axis=0)
     S = float(spread.max())
     m = tpthip.Model(ctx, gguf_1b, max_ctx=512, kv_type=tpthip.TYPE_F32)
     try:
@@ -709,17 +718,21 @@ def test_1b_teacher_forced_decode_fp16_cache(ctx, gguf_1b):
     tokens (the oracle with candle's f32 cache).  Two bars:
       * against the oracle run with the same fp16 rounding of the cache: GPU logits within S16,
         the largest max-abs distance over all steps between that run and the same run in
-        candle's two other plausible orders (no FMA in attention; block-reduced dots);
+        the other plausible orders (no FMA in attention; block-reduced dots; tree-ordered
+        RMSNorm sum of squares; all three at once);
       * against candle itself (f32 cache): the fp16 cache is a different arithmetic, and on this
         model it moves candle's logits by D, the largest distance over all steps between any of
-        the oracle's three fp16-cache runs and candle's f32 run.  The GPU's greedy token equals
+        the oracle's five fp16-cache runs and candle's f32 run.  The GPU's greedy token equals
         candle's at every step whose top-two margin exceeds D."""
     nt = min(os.cpu_count() or 1, 16)
     ref_toks = _greedy_1b(gguf_1b, nt)
     ref32 = _forced_logits(gguf_1b, PROMPT_1B, ref_toks, nthreads=nt)
     ref16 = _forced_logits(gguf_1b, PROMPT_1B, ref_toks, nthreads=nt, kv_f16=True)
     alt16 = [_forced_logits(gguf_1b, PROMPT_1B, ref_toks, fma=False, nthreads=nt, kv_f16=True),
-             _forced_logits(gguf_1b, PROMPT_1B, ref_toks, block_order=True, nthreads=nt, kv_f16=True)]
+             _forced_logits(gguf_1b, PROMPT_1B, ref_toks, block_order=True, nthreads=nt, kv_f16=True),
+             _forced_logits(gguf_1b, PROMPT_1B, ref_toks, rms_order=True, nthreads=nt, kv_f16=True),
+             _forced_logits(gguf_1b, PROMPT_1B, ref_toks, fma=False, block_order=True, rms_order=True,
+                            nthreads=nt, kv_f16=True)]
     S16 = max(float(np.abs(a - ref16).max()) for a in alt16)
     D = max(float(np.abs(c - ref32).max()) for c in [ref16] + alt16)
     got, gtok = _gpu_forced(ctx, gguf_1b, ref_toks, tpthip.TYPE_F16)

@@ -284,3 +284,36 @@ def test_repeat_penalty_applies_per_occurrence():
     out = oracle.repeat_penalty(lg, [0, 0, 1], 2.0)
     assert list(out) == [0.5, -4.0, 1.0]
     assert list(oracle.repeat_penalty(lg, [0, 1], 1.0)) == list(lg)
+
+
+def test_rms_order_instrument():
+    """The RMSNorm order probe changes only the f32 order of sum(x^2): with it on, m equals the
+    16-run + pairwise-tree sum computed here in float64-exact steps rounded as the oracle
+    rounds, and every output stays within a few ulps of candle's sequential order."""
+    rng = np.random.default_rng(11)
+    n = 4096
+    x = (rng.standard_normal(n) * 3).astype(np.float32)
+    w = np.ones(n, np.float32)
+    base = oracle.rmsnorm(x, w, 1e-5)
+    oracle.set_rms_order(True)
+    try:
+        tree = oracle.rmsnorm(x, w, 1e-5)
+    finally:
+        oracle.set_rms_order(False)
+    # the tree order by hand: fmaf runs of 16 (a*b exact in float64, one rounding to f32 per step)
+    runs = []
+    for j in range(n // 16):
+        s = np.float32(0)
+        for v in x[16 * j:16 * j + 16]:
+            s = np.float32(np.float64(v) * np.float64(v) + np.float64(s))
+        runs.append(s)
+    p = runs
+    while len(p) > 1:
+        q = [np.float32(p[2 * i] + p[2 * i + 1]) for i in range(len(p) // 2)]
+        if len(p) % 2:
+            q.append(p[-1])
+        p = q
+    m = np.sqrt(np.float32(p[0] / np.float32(n) + np.float32(1e-5)), dtype=np.float32)
+    assert np.array_equal(tree, (x / m * w).astype(np.float32))
+    ulp = np.spacing(np.abs(base)).astype(np.float64)
+    assert np.all(np.abs(tree.astype(np.float64) - base) <= 4 * ulp + 1e-30)

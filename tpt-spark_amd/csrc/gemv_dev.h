@@ -159,9 +159,11 @@ __device__ __forceinline__ void barrier_lds() {
 //    of wave w holds elements 16(l%16) .. +15 of block 4(w + qi NW) + l/16, qi < MAXQ.
 //  * Q8_0 activations: one float4 per lane per 256-element block, blocks w, w + NW, ...
 constexpr int MAXQ = MAXB / 4;  // block quads per wave in the ROWS16 layout
+constexpr int SSQL = kSsqMax / WAVE;  // RMSNorm partial sums per lane
 struct XPre {
   float4 x[MAXB];
   float4 w[MAXB];
+  float ssq[SSQL];
 };
 
 template <bool ROWS16, bool NORM>
@@ -170,6 +172,12 @@ __device__ __forceinline__ void preload_x(const GemvArgs& A, XPre& p) {
   const int nb = A.K / 256;
   const float4* xs = (const float4*)A.x;
   const float4* ws = (const float4*)A.norm_w;
+  if constexpr (NORM) {
+    if (A.ssq_in) {
+#pragma unroll
+      for (int i = 0; i < SSQL; i++) p.ssq[i] = A.ssq_in[min(lane + i * WAVE, A.n_ssq - 1)];
+    }
+  }
   if constexpr (ROWS16) {
     const int k = lane >> 4, m = lane & 15;
 #pragma unroll
@@ -201,13 +209,23 @@ __device__ __forceinline__ bool slot_valid(int i, int nb) {
   else return wid + i * NW < nb;
 }
 
-// 1/m of rms_norm (candle_nn::ops::rms_norm: m = sqrt(sum(x^2)/dim + eps)).  Every workgroup
-// reduces the whole vector itself from the preloaded registers (each element is owned by
-// exactly one lane of the workgroup).
+// 1/m of rms_norm (candle_nn::ops::rms_norm: m = sqrt(sum(x^2)/dim + eps)).  With partial sums
+// from the kernel that wrote x (A.ssq_in), every wave adds them in the same order (lane slots in
+// sequence, then the lanes by DPP), so all waves hold the same m without a workgroup barrier.
+// Otherwise every workgroup reduces the whole vector itself from the preloaded registers (each
+// element is owned by exactly one lane of the workgroup).
 template <bool ROWS16>
 __device__ __forceinline__ float rms_denominator(const GemvArgs& A, const XPre& p, float* red) {
   const int tid = threadIdx.x, wid = tid >> 6;
   const int nb = A.K / 256;
+  if (A.ssq_in) {
+    const int lane = tid & 63;
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < SSQL; i++) t += lane + i * WAVE < A.n_ssq ? p.ssq[i] : 0.f;
+    t = wave_sum_dpp(t);
+    return sqrtf(t / (float)A.K + A.eps);
+  }
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < MAXB; i++) {
@@ -784,14 +802,37 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int 
     case EPI_STORE:
       for (int i = tid; i < nrows; i += NT) A.y[r0 + i] = row_val(i, 0);
       break;
-    case EPI_RESID:
+    case EPI_RESID: {
+      float ss = 0.f;  // sum of squares of the stored rows (A.ssq_out)
       for (int i = tid; i < nrows; i += NT) {
         float r;
         if (i == tid) r = pre_r;
         else r = A.resid[r0 + i];
-        A.y[r0 + i] = row_val(i, 0) + r;
+        const float v = row_val(i, 0) + r;
+        A.y[r0 + i] = v;
+        ss = fmaf(v, v, ss);
       }
-      break;
+      if (A.ssq_out) {
+        if (nrows <= WAVE) {  // the rows sit in wave 0
+          if (wid == 0) {
+            ss = wave_sum_dpp(ss);
+            if (lane == 0) A.ssq_out[wg] = ss;
+          }
+        } else {
+          ss = wave_sum_dpp(ss);
+          float* red = L.red;  // free after the row totals were read
+          __syncthreads();
+          if (lane == 0) red[wid] = ss;
+          __syncthreads();
+          if (tid == 0) {
+            float t = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; w++) t += red[w];
+            A.ssq_out[wg] = t;
+          }
+        }
+      }
+    } break;
     case EPI_SWIGLU:
       for (int i = tid; i < nrows; i += NT) {
         const float g = row_val(i, 0);

@@ -238,9 +238,10 @@ __global__ void __launch_bounds__(256) gemv_f32_kernel(const uint8_t* __restrict
 }
 
 // ----------------------------------------------------------------- launch
+// grid_out: when given, only the workgroup count is computed (nothing is launched)
 template <int WT, int BPP, int RB, int NMAT, int KS, int D>
 int launch_cfg(const tpt_ctx* ctx, const GemvArgs& a, int wg_per_cu, hipStream_t s,
-               hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr) {
+               hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr, int* grid_out = nullptr) {
   Geo geo;
   const int nb = a.K / QK_K;
   geo.P = (nb + BPP - 1) / BPP;
@@ -258,6 +259,10 @@ int launch_cfg(const tpt_ctx* ctx, const GemvArgs& a, int wg_per_cu, hipStream_t
     return fail(TPT_ERR_UNSUPPORTED, act_kind<WT>() == ACT_F32
                                          ? "gemv: F16 weights need K * 4 bytes of LDS (K <= 15360)"
                                          : "gemv: too many rows per workgroup for LDS");
+  if (grid_out) {
+    *grid_out = grid;
+    return TPT_OK;
+  }
   const bool norm = a.prologue == PRO_RMSNORM, one = geo.P == KS;  // one pass per k-split wave
   if (norm && one) launch_inst<WT, BPP, RB, NMAT, KS, D, true, true>(a, geo, grid, lds, s, ev0, ev1);
   else if (norm) launch_inst<WT, BPP, RB, NMAT, KS, D, true, false>(a, geo, grid, lds, s, ev0, ev1);
@@ -270,23 +275,38 @@ int launch_cfg(const tpt_ctx* ctx, const GemvArgs& a, int wg_per_cu, hipStream_t
 // Launch shape by matrix shape: BPP from the row length (short rows share a pass), RB rows per
 // step, D steps in flight per wave, one workgroup per CU.
 template <int WT, int NMAT, int RB, int D>
-int by_bpp(const tpt_ctx* ctx, const GemvArgs& a, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
+int by_bpp(const tpt_ctx* ctx, const GemvArgs& a, hipStream_t s, hipEvent_t e0, hipEvent_t e1, int* g) {
   const int nb = a.K / QK_K;
-  if (nb >= 16) return launch_cfg<WT, 16, RB, NMAT, 1, D>(ctx, a, 1, s, e0, e1);
-  if (nb >= 8) return launch_cfg<WT, 8, RB, NMAT, 1, D>(ctx, a, 1, s, e0, e1);
-  if (nb >= 4) return launch_cfg<WT, 4, RB, NMAT, 1, D>(ctx, a, 1, s, e0, e1);
-  if (nb >= 2) return launch_cfg<WT, 2, RB, NMAT, 1, D>(ctx, a, 1, s, e0, e1);
-  return launch_cfg<WT, 1, RB, NMAT, 1, D>(ctx, a, 1, s, e0, e1);
+  if (nb >= 16) return launch_cfg<WT, 16, RB, NMAT, 1, D>(ctx, a, 1, s, e0, e1, g);
+  if (nb >= 8) return launch_cfg<WT, 8, RB, NMAT, 1, D>(ctx, a, 1, s, e0, e1, g);
+  if (nb >= 4) return launch_cfg<WT, 4, RB, NMAT, 1, D>(ctx, a, 1, s, e0, e1, g);
+  if (nb >= 2) return launch_cfg<WT, 2, RB, NMAT, 1, D>(ctx, a, 1, s, e0, e1, g);
+  return launch_cfg<WT, 1, RB, NMAT, 1, D>(ctx, a, 1, s, e0, e1, g);
 }
 
 template <int WT, int NMAT>
-int dispatch_shape(const tpt_ctx* ctx, const GemvArgs& a, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
-  if constexpr (NMAT == 2) return by_bpp<WT, 2, 1, 2>(ctx, a, s, e0, e1);
-  else if constexpr (WT == TPT_TYPE_F16) return by_bpp<WT, 1, 1, 2>(ctx, a, s, e0, e1);  // 128 B per group
+int dispatch_shape(const tpt_ctx* ctx, const GemvArgs& a, hipStream_t s, hipEvent_t e0, hipEvent_t e1,
+                   int* g) {
+  if constexpr (NMAT == 2) return by_bpp<WT, 2, 1, 2>(ctx, a, s, e0, e1, g);
+  else if constexpr (WT == TPT_TYPE_F16) return by_bpp<WT, 1, 1, 2>(ctx, a, s, e0, e1, g);  // 128 B per group
   else {
-    if (a.K > 8192) return by_bpp<WT, 1, 2, 2>(ctx, a, s, e0, e1);  // long rows: two rows per step
-    return by_bpp<WT, 1, 1, 2>(ctx, a, s, e0, e1);
+    if (a.K > 8192) return by_bpp<WT, 1, 2, 2>(ctx, a, s, e0, e1, g);  // long rows: two rows per step
+    return by_bpp<WT, 1, 1, 2>(ctx, a, s, e0, e1, g);
   }
+}
+
+int dispatch_type(const tpt_ctx* ctx, int wtype, const GemvArgs& a, hipStream_t s, hipEvent_t ev0,
+                  hipEvent_t ev1, int* g) {
+  const bool two = a.epilogue == EPI_SWIGLU;
+  switch (wtype) {
+    case TPT_TYPE_Q4_K: return two ? dispatch_shape<TPT_TYPE_Q4_K, 2>(ctx, a, s, ev0, ev1, g) : dispatch_shape<TPT_TYPE_Q4_K, 1>(ctx, a, s, ev0, ev1, g);
+    case TPT_TYPE_Q6_K: return two ? dispatch_shape<TPT_TYPE_Q6_K, 2>(ctx, a, s, ev0, ev1, g) : dispatch_shape<TPT_TYPE_Q6_K, 1>(ctx, a, s, ev0, ev1, g);
+    case TPT_TYPE_Q8_0: return two ? dispatch_shape<TPT_TYPE_Q8_0, 2>(ctx, a, s, ev0, ev1, g) : dispatch_shape<TPT_TYPE_Q8_0, 1>(ctx, a, s, ev0, ev1, g);
+    case TPT_TYPE_Q5_K: return two ? dispatch_shape<TPT_TYPE_Q5_K, 2>(ctx, a, s, ev0, ev1, g) : dispatch_shape<TPT_TYPE_Q5_K, 1>(ctx, a, s, ev0, ev1, g);
+    case TPT_TYPE_Q4_0: return two ? dispatch_shape<TPT_TYPE_Q4_0, 2>(ctx, a, s, ev0, ev1, g) : dispatch_shape<TPT_TYPE_Q4_0, 1>(ctx, a, s, ev0, ev1, g);
+    case TPT_TYPE_F16: return two ? dispatch_shape<TPT_TYPE_F16, 2>(ctx, a, s, ev0, ev1, g) : dispatch_shape<TPT_TYPE_F16, 1>(ctx, a, s, ev0, ev1, g);
+  }
+  return fail(TPT_ERR_UNSUPPORTED, "gemv: weight type must be Q4_K, Q5_K, Q6_K, Q8_0, Q4_0 or F16");
 }
 
 }  // namespace
@@ -300,16 +320,16 @@ int launch_gemv_q8(const tpt_ctx* ctx, int wtype, const GemvArgs& a, hipStream_t
   if (a.epilogue == EPI_SWIGLU && !a.w1) return fail(TPT_ERR_INVALID, "gemv: swiglu needs two matrices");
   if (a.epilogue == EPI_ROPE_QKV && ((a.N & 1) || (a.row0 & 1) || (a.hd & 1)))
     return fail(TPT_ERR_INVALID, "gemv: rope epilogue needs even row counts");
-  const bool two = a.epilogue == EPI_SWIGLU;
-  switch (wtype) {
-    case TPT_TYPE_Q4_K: return two ? dispatch_shape<TPT_TYPE_Q4_K, 2>(ctx, a, s, ev0, ev1) : dispatch_shape<TPT_TYPE_Q4_K, 1>(ctx, a, s, ev0, ev1);
-    case TPT_TYPE_Q6_K: return two ? dispatch_shape<TPT_TYPE_Q6_K, 2>(ctx, a, s, ev0, ev1) : dispatch_shape<TPT_TYPE_Q6_K, 1>(ctx, a, s, ev0, ev1);
-    case TPT_TYPE_Q8_0: return two ? dispatch_shape<TPT_TYPE_Q8_0, 2>(ctx, a, s, ev0, ev1) : dispatch_shape<TPT_TYPE_Q8_0, 1>(ctx, a, s, ev0, ev1);
-    case TPT_TYPE_Q5_K: return two ? dispatch_shape<TPT_TYPE_Q5_K, 2>(ctx, a, s, ev0, ev1) : dispatch_shape<TPT_TYPE_Q5_K, 1>(ctx, a, s, ev0, ev1);
-    case TPT_TYPE_Q4_0: return two ? dispatch_shape<TPT_TYPE_Q4_0, 2>(ctx, a, s, ev0, ev1) : dispatch_shape<TPT_TYPE_Q4_0, 1>(ctx, a, s, ev0, ev1);
-    case TPT_TYPE_F16: return two ? dispatch_shape<TPT_TYPE_F16, 2>(ctx, a, s, ev0, ev1) : dispatch_shape<TPT_TYPE_F16, 1>(ctx, a, s, ev0, ev1);
-  }
-  return fail(TPT_ERR_UNSUPPORTED, "gemv: weight type must be Q4_K, Q5_K, Q6_K, Q8_0, Q4_0 or F16");
+  if (a.prologue == PRO_RMSNORM && a.ssq_in && (a.n_ssq < 1 || a.n_ssq > kSsqMax))
+    return fail(TPT_ERR_INVALID, "gemv: rmsnorm partial sums must number 1 .. 256");
+  return dispatch_type(ctx, wtype, a, s, ev0, ev1, nullptr);
+}
+
+int gemv_grid(const tpt_ctx* ctx, int wtype, const GemvArgs& a) {
+  if (a.K <= 0 || a.N <= 0 || a.K % 256 || a.K > 64 * 256) return 0;
+  int g = 0;
+  if (dispatch_type(ctx, wtype, a, nullptr, nullptr, nullptr, &g) != TPT_OK) return 0;
+  return g;
 }
 
 int launch_gemv_f32(int wtype, const uint8_t* w, const float* x, float* y, int K, int N,

@@ -27,10 +27,12 @@ static_assert(offsetof(StepState, next_pos) == 4 && offsetof(StepState, parity) 
 __global__ void __launch_bounds__(256) step_begin_kernel(StepState* st, const uint32_t* prompt,
                                                          int embd_type, const uint8_t* embd,
                                                          size_t embd_row_bytes, int H, int vocab,
-                                                         float* x, uint32_t* tok_log) {
+                                                         float* x, uint32_t* tok_log, float* ssq,
+                                                         int n_ssq) {
   extern __shared__ __align__(16) uint16_t s_row[];
   __shared__ uint32_t s_tok;
   __shared__ int s_pos;
+  __shared__ float s_ss[256 / WAVE];
   if (threadIdx.x == 0) {
     const uint4* sw = (const uint4*)st;  // 256-byte aligned in the runtime buffer
     const uint4 w0 = sw[0], w1 = sw[1], w2 = sw[2];
@@ -49,7 +51,23 @@ __global__ void __launch_bounds__(256) step_begin_kernel(StepState* st, const ui
   const int nh = (int)(embd_row_bytes / 2);
   for (int i = threadIdx.x; i < nh; i += blockDim.x) s_row[i] = row[i];
   __syncthreads();
-  for (int i = threadIdx.x; i < H; i += blockDim.x) x[i] = dequant_elem(embd_type, (const uint8_t*)s_row, i);
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < H; i += blockDim.x) {
+    const float v = dequant_elem(embd_type, (const uint8_t*)s_row, i);
+    x[i] = v;
+    ss = fmaf(v, v, ss);
+  }
+  if (ssq) {  // sum(x^2) for the first layer's RMSNorm: the total in slot 0, zeros after it
+    ss = wave_sum_dpp(ss);
+    if ((threadIdx.x & 63) == 0) s_ss[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    for (int i = threadIdx.x; i < n_ssq; i += blockDim.x) {
+      float t = 0.f;
+      if (i == 0)
+        for (int w = 0; w < 256 / WAVE; w++) t += s_ss[w];
+      ssq[i] = t;
+    }
+  }
   if (threadIdx.x == 0) {
     const int np = st->parity ^ 1;
     st->pos = s_pos;
@@ -194,11 +212,12 @@ int launch_dequant(int type, const void* w, float* y, int64_t n, hipStream_t s) 
 
 int launch_step_begin(StepState* st, const uint32_t* prompt, int embd_type, const uint8_t* embd,
                       size_t embd_row_bytes, int H, int vocab, float* x, uint32_t* tok_log,
-                      hipStream_t s) {
+                      float* ssq, int n_ssq, hipStream_t s) {
   if (embd_row_bytes % 2 || embd_row_bytes > 65536)
     return fail(TPT_ERR_UNSUPPORTED, "embedding rows must be of even length and at most 64 KB");
+  if (ssq && (n_ssq < 1 || n_ssq > kSsqMax)) return fail(TPT_ERR_INVALID, "step begin: 1 .. 256 partial sums");
   hipLaunchKernelGGL(step_begin_kernel, dim3(1), dim3(256), embd_row_bytes, s, st, prompt,
-                     embd_type, embd, embd_row_bytes, H, vocab, x, tok_log);
+                     embd_type, embd, embd_row_bytes, H, vocab, x, tok_log, ssq, n_ssq);
   TPT_HIP(hipGetLastError());
   return TPT_OK;
 }

@@ -48,12 +48,22 @@ struct GemvArgs {
   int pos_host = 0;
   // EPI_ARGMAX
   unsigned long long* amax = nullptr;  // slot array; slot = state ? amax[state->parity] : amax[0]
+  // EPI_RESID: ssq_out[blockIdx.x] = the sum of squares of the rows the workgroup stores, so the
+  // next RMSNorm prologue can take sum(x^2) from these partials
+  float* ssq_out = nullptr;
+  // PRO_RMSNORM: sum(x^2) given as n_ssq (<= kSsqMax) partial sums; every wave adds them itself,
+  // so the prologue needs no workgroup reduction.  nullptr: the workgroup reduces x.
+  const float* ssq_in = nullptr;
+  int n_ssq = 0;
 };
+constexpr int kSsqMax = 256;
 
 // Chooses the lane layout for K and launches.  wtype in {Q4_K, Q5_K, Q6_K, Q8_0, Q4_0, F16}.  ev0/ev1, when
 // given, are timestamped by the dispatch itself (hipExtLaunchKernelGGL) around the kernel.
 int launch_gemv_q8(const tpt_ctx* ctx, int wtype, const GemvArgs& a, hipStream_t s,
                    hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
+// The workgroup count launch_gemv_q8 would use for this type and shape (0 if it would fail).
+int gemv_grid(const tpt_ctx* ctx, int wtype, const GemvArgs& a);
 int launch_gemv_f32(int wtype, const uint8_t* w, const float* x, float* y, int K, int N,
                     hipStream_t s);
 
@@ -158,51 +168,10 @@ struct QkvPostArgs {
 };
 int launch_qkv_post(const QkvPostArgs& a, hipStream_t s);
 
+// ssq (optional): n_ssq slots receive sum(x^2) in slot 0 and zeros after it, the partial-sum
+// form the first layer's RMSNorm prologue reads (GemvArgs::ssq_in).
 int launch_step_begin(StepState* st, const uint32_t* prompt, int embd_type,
                       const uint8_t* embd, size_t embd_row_bytes, int H, int vocab, float* x,
-                      uint32_t* tok_log, hipStream_t s);
-
-// ---- persistent decode step (k_decode.hip): token embedding and every decoder layer of one
-// decode step in a single launch of one workgroup per compute unit, phases separated by
-// grid barriers.  The LM head runs after it as its own GEMV launch.
-struct DecLayer {
-  const uint8_t* qkv = nullptr;  // q|k|v rows adjacent, Q4_K
-  const uint8_t* o = nullptr;
-  const uint8_t* gate = nullptr;
-  const uint8_t* up = nullptr;
-  const uint8_t* down = nullptr;
-  const float* attn_norm = nullptr;
-  const float* ffn_norm = nullptr;
-};
-struct DecodeArgs {
-  const DecLayer* layers = nullptr;  // device array [n_layers]
-  int n_layers = 0;
-  int H = 0, qd = 0, kd = 0, hd = 0, nq = 0, nkv = 0, F = 0, max_ctx = 0, vocab = 0;
-  float eps = 0.f, attn_scale = 0.f;
-  const uint8_t* embd = nullptr;
-  int embd_type = 0;
-  size_t embd_row = 0;
-  void* kv = nullptr;            // [layer][K|V][nkv][max_ctx][hd]
-  int kv_type = TPT_TYPE_F16;
-  size_t layer_kv_bytes = 0;     // K and V of one layer
-  float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *part = nullptr;
-  const float *rope_cos = nullptr, *rope_sin = nullptr;
-  StepState* st = nullptr;
-  const uint32_t* prompt = nullptr;
-  uint32_t* tok_log = nullptr;
-  unsigned* flags = nullptr;     // [grid] arrival epochs, one per 128-byte line
-  unsigned* epoch = nullptr;     // barrier epoch the next launch starts from (advanced by it)
-  unsigned* err = nullptr;       // non-zero after a barrier wait timed out
-  int n_chunks = 0, chunk_len = 0;
-  int rpw_qkv = 0, rpw_o = 0, rpw_gu = 0, rpw_dn = 0;  // rows per workgroup of each phase
-  size_t s_h = 0, s_q = 0, s_f = 0;  // weight row bytes for K = H, K = qd, K = F
-  int grid = 0, lds = 0;             // filled by decode_layers_plan
-};
-// Grid-barrier arrivals one decode-layers launch makes (its epochs advance bar_base by this).
-__host__ __device__ inline int decode_layers_barriers(int n_layers) { return 6 * n_layers - 1; }
-// Checks the shape against the compiled instantiations and fills grid, rows per workgroup and
-// the LDS size (n_chunks / chunk_len set first).  TPT_ERR_UNSUPPORTED when no kernel fits.
-int decode_layers_plan(const tpt_ctx* ctx, DecodeArgs& a);
-int launch_decode_layers(const DecodeArgs& a, hipStream_t s);
+                      uint32_t* tok_log, float* ssq, int n_ssq, hipStream_t s);
 
 }  // namespace tpt

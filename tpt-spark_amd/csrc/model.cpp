@@ -53,7 +53,6 @@ tpt_model::~tpt_model() {
   if (arena) (void)hipFree(arena);
   if (runtime) (void)hipFree(runtime);
   if (pf_mem) (void)hipFree(pf_mem);
-  if (dec_mem) (void)hipFree(dec_mem);
   if (st_host) (void)hipHostFree(st_host);
   if (ids_host) (void)hipHostFree(ids_host);
 }
@@ -291,7 +290,8 @@ int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_t
                o_lg = carve((size_t)desc.vocab * 4), o_rc = carve((size_t)max_ctx * hd / 2 * 4),
                o_rs = carve((size_t)max_ctx * hd / 2 * 4), o_st = carve(sizeof(StepState)),
                o_pr = carve((size_t)max_ctx * 4), o_tl = carve((size_t)max_ctx * 4),
-               o_ap = carve((size_t)attn_part_floats(nq, nkv, hd, attn_max_chunks) * 4);
+               o_ap = carve((size_t)attn_part_floats(nq, nkv, hd, attn_max_chunks) * 4),
+               o_ss = carve((size_t)2 * kSsqMax * 4);
   TPT_HIP(hipMalloc(&runtime, ro));
   uint8_t* R = (uint8_t*)runtime;
   kv = R + o_kv;
@@ -306,6 +306,8 @@ int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_t
   prompt_dev = (uint32_t*)(R + o_pr);
   tok_log = (uint32_t*)(R + o_tl);
   attn_part = (float*)(R + o_ap);
+  ssq_a = (float*)(R + o_ss);
+  ssq_b = ssq_a + kSsqMax;
   TPT_HIP(hipMemsetAsync(runtime, 0, ro, stream));  // load time, outside any graph
 
   // RoPE tables exactly as quantized_llama::precomput_freqs_cis: f32 theta = 1/base^(2i/d)
@@ -340,108 +342,18 @@ int tpt_model::load(tpt_ctx* c, const char* gguf_path, int max_ctx_req, int kv_t
   causal_mfma = !(ev_att && strcmp(ev_att, "splitk") == 0);
   const char* ev_graph = getenv("TPT_HIP_GRAPHS");
   use_graphs = !(ev_graph && ev_graph[0] == '0');
-  if ((rc = setup_decode_layers())) return rc;
   TPT_HIP(hipStreamSynchronize(stream));
   return TPT_OK;
 }
 
-// The persistent decode step needs every layer matrix in Q4_K with q|k|v adjacent, q width =
-// embedding width, and a compiled instantiation whose LDS fits every length bucket's attention
-// partition.  It is selected with TPT_HIP_DECODE=persistent or tpt_model_set_decode_path.
-int tpt_model::setup_decode_layers() {
-  decode_layers_ok = use_decode_layers = false;
-  const int H = desc.embed, hd = desc.head_dim, nq = desc.n_heads, nkv = desc.n_kv_heads;
-  const int qd = nq * hd, kd = nkv * hd, mc = desc.max_ctx;
-  for (const Layer& L : layers) {
-    if (!L.qkv_adjacent) return TPT_OK;
-    for (int t : {L.tq, L.to, L.tg, L.tu, L.td})
-      if (t != TPT_TYPE_Q4_K) return TPT_OK;
-  }
-  DecodeArgs d;
-  d.n_layers = desc.n_layers;
-  d.H = H; d.qd = qd; d.kd = kd; d.hd = hd; d.nq = nq; d.nkv = nkv; d.F = desc.ffn;
-  d.max_ctx = mc; d.vocab = desc.vocab;
-  d.eps = desc.rms_eps;
-  d.attn_scale = (float)(1.0 / sqrt((double)hd));  // the scale launch_attn_decode uses
-  d.embd = embd; d.embd_type = embd_type; d.embd_row = embd_row;
-  d.kv = kv; d.kv_type = desc.kv_type; d.layer_kv_bytes = (size_t)2 * nkv * mc * hd * kv_elem;
-  d.x = x; d.q = qbuf; d.att = attn; d.h = hbuf; d.part = attn_part;
-  d.rope_cos = rope_cos; d.rope_sin = rope_sin;
-  d.st = st; d.prompt = prompt_dev; d.tok_log = tok_log;
-  d.s_h = row_bytes(TPT_TYPE_Q4_K, H); d.s_q = row_bytes(TPT_TYPE_Q4_K, qd);
-  d.s_f = row_bytes(TPT_TYPE_Q4_K, desc.ffn);
-  for (int L = 1; L <= mc; L = bucket_of(L) + 1) {  // every bucket's partition must fit
-    DecodeArgs t = d;
-    const int b = bucket_of(L);
-    t.n_chunks = std::min(attn_default_chunks(b, nkv), attn_max_chunks);
-    t.chunk_len = attn_chunk_len(b, t.n_chunks);
-    if (decode_layers_plan(ctx, t) != TPT_OK) {
-      set_error("");  // not an error: this model decodes with one launch per op
-      return TPT_OK;
-    }
-    if (L == 1) d.grid = t.grid;
-  }
-  // barrier state (flags, epoch, error word: one 128-byte line each), then the layer table
-  const size_t line = 128;
-  dec_sync_bytes = line * ((size_t)d.grid + 2);
-  const size_t tab = sizeof(DecLayer) * desc.n_layers;
-  TPT_HIP(hipMalloc(&dec_mem, dec_sync_bytes + tab));
-  uint8_t* m = (uint8_t*)dec_mem;
-  d.flags = (unsigned*)m;
-  d.epoch = (unsigned*)(m + line * d.grid);
-  d.err = (unsigned*)(m + line * (d.grid + 1));
-  d.layers = (const DecLayer*)(m + dec_sync_bytes);
-  std::vector<DecLayer> t(desc.n_layers);
-  for (int l = 0; l < desc.n_layers; l++) {
-    const Layer& L = layers[l];
-    t[l].qkv = L.q; t[l].o = L.o; t[l].gate = L.gate; t[l].up = L.up; t[l].down = L.down;
-    t[l].attn_norm = L.attn_norm; t[l].ffn_norm = L.ffn_norm;
-  }
-  TPT_HIP(hipMemcpyAsync(m + dec_sync_bytes, t.data(), tab, hipMemcpyHostToDevice, stream));
-  TPT_HIP(hipStreamSynchronize(stream));
-  dec = d;
-  int rc = dec_reset();
-  if (rc) return rc;
-  decode_layers_ok = true;
-  // measured on the 8B shape at 2K positions: 1.93 ms/token with one launch per op, 2.09 ms with
-  // the persistent kernel, so the per-op launches stay the default
-  const char* ev = getenv("TPT_HIP_DECODE");
-  use_decode_layers = ev && strcmp(ev, "persistent") == 0;
-  return TPT_OK;
-}
-
-int tpt_model::dec_reset() {
-  TPT_HIP(hipStreamSynchronize(stream));
-  TPT_HIP(hipMemsetAsync(dec_mem, 0, dec_sync_bytes, stream));  // outside any graph
-  TPT_HIP(hipStreamSynchronize(stream));
-  dec_epochs = 0;
-  return TPT_OK;
-}
-
-int tpt_model::dec_check() {
-  if (!decode_layers_ok) return TPT_OK;
-  unsigned err = 0;
-  TPT_HIP(hipMemcpyAsync(&err, dec.err, 4, hipMemcpyDeviceToHost, stream));
-  TPT_HIP(hipStreamSynchronize(stream));
-  if (!err) return TPT_OK;
-  int rc = dec_reset();
-  if (rc) return rc;
-  return fail(TPT_ERR_HIP, "decode step: a grid barrier wait timed out (not every workgroup of the persistent kernel was resident); results of this call are invalid");
-}
-
+// One launch per fused op is the only decode form: a persistent kernel (embedding and every layer
+// in one launch, grid barriers between the phases) decoded the 8B shape at 476-488 tok/s
+// against 586-592 and was removed; TPT_DECODE_PERSISTENT is refused.
 int tpt_model::set_decode_path(int path) {
-  if (path != TPT_DECODE_KERNELS && path != TPT_DECODE_PERSISTENT)
-    return fail(TPT_ERR_INVALID, "decode path must be TPT_DECODE_KERNELS or TPT_DECODE_PERSISTENT");
-  if (path == TPT_DECODE_PERSISTENT && !decode_layers_ok)
-    return fail(TPT_ERR_UNSUPPORTED, "no persistent decode kernel for this model's shape or types");
-  const bool want = path == TPT_DECODE_PERSISTENT;
-  if (want != use_decode_layers) {
-    TPT_HIP(hipStreamSynchronize(stream));
-    for (auto& kv : graphs) (void)hipGraphExecDestroy(kv.second);
-    graphs.clear();
-    use_decode_layers = want;
-  }
-  return TPT_OK;
+  if (path == TPT_DECODE_KERNELS) return TPT_OK;
+  if (path == TPT_DECODE_PERSISTENT)
+    return fail(TPT_ERR_UNSUPPORTED, "no persistent decode kernel: decode steps run one launch per fused op");
+  return fail(TPT_ERR_INVALID, "decode path must be TPT_DECODE_KERNELS or TPT_DECODE_PERSISTENT");
 }
 
 // Attention partition of the length bucket holding L (64, 128, 256, 512, then multiples of
@@ -458,18 +370,12 @@ int tpt_model::enqueue_step(int bucket, bool lm_head) {
   const int n_chunks = std::min(attn_default_chunks(bucket, desc.n_kv_heads), attn_max_chunks);
   const int chunk_len = attn_chunk_len(bucket, n_chunks);
   int rc;
-  if (use_decode_layers) {
-    DecodeArgs d = dec;
-    d.n_chunks = n_chunks;
-    d.chunk_len = chunk_len;
-    if ((rc = decode_layers_plan(ctx, d)) || (rc = launch_decode_layers(d, stream))) return rc;
-  } else {
-    if ((rc = launch_step_begin(st, prompt_dev, embd_type, embd, embd_row, desc.embed, desc.vocab,
-                                x, tok_log, stream)))
-      return rc;
-    for (int l = 0; l < desc.n_layers; l++)
-      if ((rc = enqueue_layer(l, n_chunks, chunk_len))) return rc;
-  }
+  if ((rc = launch_step_begin(st, prompt_dev, embd_type, embd, embd_row, desc.embed, desc.vocab,
+                              x, tok_log, ssq_b, kSsqMax, stream)))
+    return rc;
+  ssq_b_n = kSsqMax;
+  for (int l = 0; l < desc.n_layers; l++)
+    if ((rc = enqueue_layer(l, n_chunks, chunk_len))) return rc;
   if (lm_head) {
     GemvArgs lh;
     lh.w0 = out;
@@ -484,6 +390,8 @@ int tpt_model::enqueue_step(int bucket, bool lm_head) {
     lh.y = logits;
     lh.amax = (unsigned long long*)((char*)st + offsetof(StepState, amax));  // device address
     lh.state = st;
+    lh.ssq_in = ssq_b_n ? ssq_b : nullptr;
+    lh.n_ssq = ssq_b_n;
     if ((rc = launch_gemv_q8(ctx, out_type, lh, stream))) return rc;
   }
   return TPT_OK;
@@ -518,6 +426,8 @@ int tpt_model::enqueue_layer(int l, int n_chunks, int chunk_len) {
     g.vcache = vc;
     g.kv_type = desc.kv_type;
     g.state = st;
+    g.ssq_in = ssq_b_n ? ssq_b : nullptr;
+    g.n_ssq = ssq_b_n;
     if (L.qkv_adjacent) {
       g.w0 = L.q;
       g.row_stride = row_bytes(L.tq, H);
@@ -560,6 +470,8 @@ int tpt_model::enqueue_layer(int l, int n_chunks, int chunk_len) {
     wo.epilogue = EPI_RESID;
     wo.y = x;
     wo.resid = x;
+    const int n_wo = gemv_grid(ctx, L.to, wo);
+    if (n_wo >= 1 && n_wo <= kSsqMax) wo.ssq_out = ssq_a;
     if ((rc = launch_gemv_q8(ctx, L.to, wo, stream))) return rc;
     // h = silu(W1 . n(x)) * (W3 . n(x))
     GemvArgs gu;
@@ -574,6 +486,10 @@ int tpt_model::enqueue_layer(int l, int n_chunks, int chunk_len) {
     gu.prologue = PRO_RMSNORM;
     gu.epilogue = EPI_SWIGLU;
     gu.y = hbuf;
+    if (wo.ssq_out) {
+      gu.ssq_in = ssq_a;
+      gu.n_ssq = n_wo;
+    }
     if ((rc = launch_gemv_q8(ctx, L.tg, gu, stream))) return rc;
     // x += W2 . h
     GemvArgs dn;
@@ -585,6 +501,9 @@ int tpt_model::enqueue_layer(int l, int n_chunks, int chunk_len) {
     dn.epilogue = EPI_RESID;
     dn.y = x;
     dn.resid = x;
+    const int n_dn = gemv_grid(ctx, L.td, dn);
+    ssq_b_n = n_dn >= 1 && n_dn <= kSsqMax ? n_dn : 0;
+    if (ssq_b_n) dn.ssq_out = ssq_b;
     if ((rc = launch_gemv_q8(ctx, L.td, dn, stream))) return rc;
   }
   return TPT_OK;
@@ -592,14 +511,6 @@ int tpt_model::enqueue_layer(int l, int n_chunks, int chunk_len) {
 
 int tpt_model::launch_step(int L, bool lm_head) {
   if (L > desc.max_ctx) return fail(TPT_ERR_STATE, "context length exhausted");
-  if (use_decode_layers) {  // barrier epochs are 32-bit: clear the state long before they wrap
-    const uint64_t nb = (uint64_t)decode_layers_barriers(desc.n_layers);
-    if (dec_epochs + nb > 0xF0000000ull) {
-      int rc = dec_reset();
-      if (rc) return rc;
-    }
-    dec_epochs += nb;
-  }
   const int nch = bucket_of(L);
   if (!use_graphs || !lm_head) return enqueue_step(nch, lm_head);
   auto it = graphs.find(nch);
@@ -835,6 +746,7 @@ int tpt_model::run_layers(const float* x_in, int n, int pos0, int l0, int l1, in
     st_host->next_pos = p + 1;
     TPT_HIP(hipMemcpyAsync(st, st_host, sizeof(StepState), hipMemcpyHostToDevice, stream));
     TPT_HIP(hipMemcpyAsync(x, x_in + (size_t)t * H, (size_t)H * 4, hipMemcpyHostToDevice, stream));
+    ssq_b_n = 0;  // x came from the host: the first RMSNorm reduces it itself
     for (int l = l0; l < l1; l++)
       if ((rc = enqueue_layer(l, nch, attn_chunk_len(bucket, nch)))) return rc;
     TPT_HIP(hipMemcpyAsync(x_out + (size_t)t * H, x, (size_t)H * 4, hipMemcpyDeviceToHost, stream));
@@ -877,7 +789,7 @@ int tpt_model::prefill(const uint32_t* ids, int n, int pos0, uint32_t* next_out,
     return rc;
   }
   StepState s;
-  if ((rc = read_state(&s)) || (rc = dec_check())) return rc;
+  if ((rc = read_state(&s))) return rc;
   if (next_out) *next_out = (uint32_t)(s.amax[s.parity] & 0xffffffffull);
   if (logits_out) {
     TPT_HIP(hipMemcpyAsync(logits_out, logits, (size_t)desc.vocab * 4, hipMemcpyDeviceToHost, stream));
@@ -930,7 +842,6 @@ int tpt_model::decode_stream(uint32_t first, int pos0, int n_steps, StepFn fn, v
   for (hipEvent_t ev : evs) (void)hipEventDestroy(ev);
   if (rc) return rc;
   if (e != hipSuccess) return hip_fail(e, "decode", __FILE__, __LINE__);
-  if ((rc = dec_check())) return rc;
   if (!stop && (rc = deliver(launched - 1))) return rc;
   if (!stop && delivered == launched - 1) {
     StepState s;
@@ -1060,7 +971,7 @@ int tpt_model_set_decode_path(tpt_model* m, int path) {
 
 int tpt_model_get_decode_path(const tpt_model* m, int* path) {
   if (!m || !path) return fail(TPT_ERR_INVALID, "null argument");
-  *path = m->use_decode_layers ? TPT_DECODE_PERSISTENT : TPT_DECODE_KERNELS;
+  *path = TPT_DECODE_KERNELS;
   return TPT_OK;
 }
 

@@ -43,6 +43,12 @@ struct tpt_model {
   uint32_t* tok_log = nullptr;     // [max_ctx] token consumed at each position
   float* attn_part = nullptr;
   int attn_max_chunks = 0;
+  // RMSNorm partial sums (GemvArgs::ssq_in): ssq_a = sum(x^2) pieces after the attention block's
+  // residual add (written by the Wo GEMV), ssq_b after the FFN block's (down GEMV, or step_begin
+  // for the first layer); ssq_b_n = how many slots of ssq_b the last writer filled (0: none,
+  // the next RMSNorm reduces x itself)
+  float *ssq_a = nullptr, *ssq_b = nullptr;
+  int ssq_b_n = 0;
   void* runtime = nullptr;  // one allocation holding the buffers above
 
   tpt::StepState* st_host = nullptr;  // pinned
@@ -50,17 +56,7 @@ struct tpt_model {
   bool use_graphs = true;
   std::map<int, hipGraphExec_t> graphs;  // by length bucket
 
-  // persistent decode step (k_decode.hip): embedding + all layers in one launch
-  bool decode_layers_ok = false;   // a persistent kernel exists for this shape
-  bool use_decode_layers = false;  // decode steps run it (else one launch per op)
-  tpt::DecodeArgs dec{};           // its arguments except the attention partition
-  void* dec_mem = nullptr;         // layer table + barrier flags, epoch, counters, error word
-  size_t dec_sync_bytes = 0;       // bytes of the barrier state at the start of dec_mem
-  uint64_t dec_epochs = 0;         // barrier epochs issued since the state was last cleared
-  int setup_decode_layers();
-  int set_decode_path(int path);
-  int dec_reset();                 // clears the barrier state (synchronizes the stream)
-  int dec_check();                 // reports a timed-out barrier wait, then clears the state
+  int set_decode_path(int path);  // TPT_DECODE_KERNELS only
 
   // batched prefill (MFMA GEMMs over up to kPrefillT positions at once)
   static constexpr int kPrefillT = 2048;

@@ -399,8 +399,8 @@ class Model:
 
     @property
     def decode_path(self):
-        """DECODE_PERSISTENT: embedding + all layers of a decode step in one launch (grid
-        barriers between phases); DECODE_KERNELS: one launch per fused op."""
+        """DECODE_KERNELS: one launch per fused op, the only decode form (DECODE_PERSISTENT,
+        a single-launch step, was removed: setting it raises TPT_ERR_UNSUPPORTED)."""
         v = C.c_int()
         check(lib().tpt_model_get_decode_path(self.h, C.byref(v)))
         return v.value
