@@ -707,13 +707,19 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& A, const Geo& geo, int 
   // the prologue then waits only for the former (left alone, the scheduler sinks some
   // activation loads below the weight loads, or hoists the first uses of x above them)
   __builtin_amdgcn_sched_barrier(0);
+  // Long rows (two rows per step, K > 8192: the down GEMV's 56 KB activation) issue one step
+  // ahead of the prologue and the rest behind it, so fewer weight bytes stand between the
+  // activation loads and the prologue (8B decode +1%); shorter rows issue all D ahead.
+  constexpr int PRE = RB == 2 ? 1 : D;
 #pragma unroll
-  for (int d = 0; d < D; d++) issue(ring[d], d);
+  for (int d = 0; d < PRE; d++) issue(ring[d], d);
   __builtin_amdgcn_sched_barrier(0);
   hook();
   if constexpr (act_kind<WT>() == ACT_F32) prologue_f32<NORM ? 1 : 0>(A, xp, L);
   else if constexpr (act_q80<WT>()) prologue_q80<NORM ? 1 : 0>(A, xp, L);
   else prologue_q8k<NORM ? 1 : 0>(A, xp, L);
+#pragma unroll
+  for (int d = PRE; d < D; d++) issue(ring[d], d);
   barrier_lds();
 
   // EPI_ROPE_QKV: the rotation of the thread's first (even, odd) row pair, issued behind the

@@ -17,7 +17,9 @@
 //    trip).
 //    Scores go to LDS; after the chunk max, p = exp(s - max) is formed once per (head,
 //    position) and summed; then o = sum p v.  The record (o unnormalised, max, sum) goes to
-//    the partial buffer.
+//    the partial buffer.  Chunks of up to 64 positions (the decode partition up to 4096
+//    positions with 8 kv heads) take attn_partial1: the chunk's K and V rows, scores and
+//    probabilities stay in registers, two workgroup barriers instead of four.
 //  * attn_merge, one workgroup per 32 output dims: combines the chunk records with the
 //    log-sum-exp rule; its first chunk loads are issued before the chunk weights are known.  The kernel boundary orders the two, so
 //    no device-wide fence or arrival counter is needed.
@@ -195,6 +197,121 @@ __global__ void __launch_bounds__(ANT) attn_partial_kernel(const AttnArgs a, con
   }
 }
 
+// The same record in one pass when the chunk fits the registers (chunk_len <= R*U): every thread
+// keeps the scores of its U positions, forms p = exp(s - max) for them once the chunk max is
+// known and accumulates p and p*v at once.  Two workgroup barriers (the max, then the record's
+// sums over position groups) instead of four, and no score round trip through LDS.
+template <typename T, int HD, int G, int U>
+__global__ void __launch_bounds__(ANT) attn_partial1_kernel(const AttnArgs a, const float scale) {
+  constexpr int LPP = KvTraits<T>::LPP;
+  constexpr int EPL = HD / LPP;
+  constexpr int R = ANT / LPP;
+  constexpr int PSTRIDE = HD + 2;
+  __shared__ float s_red[ANW][G];
+  __shared__ float s_l[ANW][G];
+  __shared__ float s_o[R][G][HD];
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int li = tid % LPP, pg = tid / LPP;
+  const int kvh = blockIdx.y, chunk = blockIdx.x, nch = gridDim.x, t = blockIdx.z;
+  const int CL = a.chunk_len;
+  const int p0 = chunk * CL;
+  const int plast = min(p0 + CL, a.L_stride) - 1;
+  const T* K = (const T*)a.kc + (size_t)kvh * a.L_stride * HD + li * EPL;
+  const T* V = (const T*)a.vc + (size_t)kvh * a.L_stride * HD + li * EPL;
+
+  float q[G][EPL];
+#pragma unroll
+  for (int h = 0; h < G; h++)
+#pragma unroll
+    for (int e = 0; e < EPL; e++) q[h][e] = a.q[(size_t)t * a.ldq + (size_t)(kvh * G + h) * HD + li * EPL + e];
+  float kk[U][EPL], vv[U][EPL];
+#pragma unroll
+  for (int u = 0; u < U; u++) load_row<EPL>(K + (size_t)min(p0 + u * R + pg, plast) * HD, kk[u]);
+#pragma unroll
+  for (int u = 0; u < U; u++) load_row<EPL>(V + (size_t)min(p0 + u * R + pg, plast) * HD, vv[u]);
+
+  const int L = (a.state ? a.state->pos + 1 : a.L_host) + t;
+  const int p1 = min(L, p0 + CL);
+  if (p1 <= p0) return;  // a chunk past the live length: the merge does not read its record
+
+  float sc[U][G], mloc[G];
+#pragma unroll
+  for (int h = 0; h < G; h++) mloc[h] = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const bool live = p0 + u * R + pg < p1;
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+      float d = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; e++) d = fmaf(q[h][e], kk[u][e], d);
+      sc[u][h] = lane_group_sum<LPP>(d) * scale;
+      if (live) mloc[h] = fmaxf(mloc[h], sc[u][h]);
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < G; h++) {
+    const float m = wave_max_dpp(mloc[h]);
+    if (lane == 0) s_red[wid][h] = m;
+  }
+  __syncthreads();
+  float M[G];
+#pragma unroll
+  for (int h = 0; h < G; h++) {
+    M[h] = s_red[0][h];
+#pragma unroll
+    for (int w = 1; w < ANW; w++) M[h] = fmaxf(M[h], s_red[w][h]);
+  }
+
+  float o[G][EPL], ls[G];
+#pragma unroll
+  for (int h = 0; h < G; h++) {
+    ls[h] = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; e++) o[h][e] = 0.f;
+  }
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    if (p0 + u * R + pg < p1) {
+#pragma unroll
+      for (int h = 0; h < G; h++) {
+        const float w = expf(sc[u][h] - M[h]);
+        ls[h] += w;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) o[h][e] = fmaf(w, vv[u][e], o[h][e]);
+      }
+    }
+  }
+  // the LPP lanes of a position group hold the same sums: count each group once
+#pragma unroll
+  for (int h = 0; h < G; h++) {
+    const float l = wave_sum_dpp(li == 0 ? ls[h] : 0.f);
+    if (lane == 0) s_l[wid][h] = l;
+  }
+#pragma unroll
+  for (int h = 0; h < G; h++)
+#pragma unroll
+    for (int e = 0; e < EPL; e++) s_o[pg][h][li * EPL + e] = o[h][e];
+  __syncthreads();
+
+  float* part = a.part + (((size_t)t * gridDim.y + kvh) * nch + chunk) * G * PSTRIDE;
+  for (int i = tid; i < G * HD; i += ANT) {
+    const int h = i / HD, d = i % HD;
+    float s = 0.f;
+#pragma unroll
+    for (int g = 0; g < R; g++) s += s_o[g][h][d];
+    part[h * PSTRIDE + d] = s;
+  }
+  if (tid < G) {
+    float l = 0.f;
+#pragma unroll
+    for (int w = 0; w < ANW; w++) l += s_l[w][tid];
+    part[tid * PSTRIDE + HD] = M[tid];
+    part[tid * PSTRIDE + HD + 1] = l;
+  }
+}
+
 // o[h][d] = sum_c w_c o_c[h][d] / sum_c w_c l_c with w_c = exp(m_c - max_c m_c).  Workgroup:
 // 32 consecutive output dims of one head; thread (set, j) sums chunks set, set + 8, ...
 template <int HD, int G>
@@ -280,7 +397,10 @@ template <typename T, int HD, int G>
 int launch_g(const AttnArgs& a, float scale, hipStream_t s) {
   const dim3 grid((unsigned)a.n_chunks, (unsigned)a.nkv, (unsigned)a.nqb);
   constexpr int R = ANT / KvTraits<T>::LPP;
-  if (a.chunk_len <= 4 * R)
+  constexpr int U1 = 64 / R;  // one-pass form: chunks of up to 64 positions
+  if (a.chunk_len <= U1 * R)
+    hipLaunchKernelGGL((attn_partial1_kernel<T, HD, G, U1>), grid, dim3(ANT), 0, s, a, scale);
+  else if (a.chunk_len <= 4 * R)
     hipLaunchKernelGGL((attn_partial_kernel<T, HD, G, 4>), grid, dim3(ANT), 0, s, a, scale);
   else
     hipLaunchKernelGGL((attn_partial_kernel<T, HD, G, 8>), grid, dim3(ANT), 0, s, a, scale);
