@@ -272,10 +272,11 @@ def main():
     ap.add_argument("--prompt", type=int, default=PROMPT_LEN)
     ap.add_argument("--model", default="", help="existing GGUF (default: generate the 8B shape)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--leg", choices=["all", "gemv", "attn", "gemm", "causal"], default="all",
+    ap.add_argument("--leg", choices=["all", "gemv", "attn", "gemm", "causal", "decode"], default="all",
                     help="gemv: only the GEMV roofline leg and the copy calibration (profiling); "
                          "attn: only the decode-attention leg; gemm: only the prefill GEMM leg; "
-                         "causal: only the prompt-attention leg")
+                         "causal: only the prompt-attention leg; decode: only the end-to-end "
+                         "prefill + decode run (profiling; no roofline or CPU legs)")
     ap.add_argument("--gemv-iters", type=int, default=256, help="timed launches per GEMV shape")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -298,15 +299,17 @@ def main():
     if args.leg == "causal":
         print(json.dumps({"prefill_attn": attn_causal_roofline(tp, ctx)}))
         return
-    gemv = gemv_roofline(tp, ctx, iters=args.gemv_iters)
-    if args.leg == "gemv":
-        print(json.dumps({"gemv": gemv, "copy": copy_calibration(ctx)}))
-        return
-    gemv_q6k = gemv_roofline(tp, ctx, iters=64, qtype=tp.TYPE_Q6_K)
-    gemv_q80 = gemv_roofline(tp, ctx, iters=64, qtype=tp.TYPE_Q8_0)
-    attn = attn_roofline(tp, ctx)
-    gemm = gemm_roofline(tp, ctx)
-    causal = attn_causal_roofline(tp, ctx)
+    decode_only = args.leg == "decode"
+    if not decode_only:
+        gemv = gemv_roofline(tp, ctx, iters=args.gemv_iters)
+        if args.leg == "gemv":
+            print(json.dumps({"gemv": gemv, "copy": copy_calibration(ctx)}))
+            return
+        gemv_q6k = gemv_roofline(tp, ctx, iters=64, qtype=tp.TYPE_Q6_K)
+        gemv_q80 = gemv_roofline(tp, ctx, iters=64, qtype=tp.TYPE_Q8_0)
+        attn = attn_roofline(tp, ctx)
+        gemm = gemm_roofline(tp, ctx)
+        causal = attn_causal_roofline(tp, ctx)
 
     tmpdir = tempfile.mkdtemp(prefix="tpt_bench_", dir=os.environ.get("TPT_BENCH_DIR") or None)
     path = args.model
@@ -348,7 +351,7 @@ def main():
         log(f"prefill {len(prompt)} tok in {st.ttft_ms:.0f} ms ({prefill_tok_s:.1f} tok/s); decode "
             f"{args.steps} tok in {st.decode_ms:.1f} ms = {tok_s:.1f} tok/s; ceiling {ceiling:.1f}")
         eng.close()
-        cpu = None if args.no_cpu else cpu_baseline(path, len(prompt))
+        cpu = None if (args.no_cpu or decode_only) else cpu_baseline(path, len(prompt))
     finally:
         if not args.model and os.path.exists(path):
             os.remove(path)
@@ -357,6 +360,10 @@ def main():
         except OSError:
             pass
 
+    if decode_only:
+        print(json.dumps({"decode_tok_s": round(tok_s, 2), "ms_per_step": round(st.decode_ms / args.steps, 4),
+                          "prefill_tok_s": round(prefill_tok_s, 2), "decode_ceiling_tok_s": round(ceiling, 1)}))
+        return
     g = gemv["4096x14336"]
     line = {
         "metric": METRIC,
