@@ -921,6 +921,15 @@ __device__ __forceinline__ void wide_phase(const GemmArgs& g, const WideOff& o, 
   wide_store<MODE, (S + 1) % 4>(st, s.b[(S + 1) & 1], s.blk[S == 3 ? (kb + 1) & 1 : kb & 1]);
   wide_dma_a<(S + 2) % 4>(g, o, m0, kb2, s.a[ia2]);
   wide_load<MODE, (S + 2) % 4>(g, o, kb2, st);
+  // the two waves of a SIMD reach the barrier together, so their MFMAs and their VALU work
+  // (the next tile's decode, the block end) cannot overlap each other; inside each wave, six
+  // VALU instructions after every MFMA keep the VALU busy while the matrix core runs
+  // (q8k M=2048: +2-3% against the compiler's own order; 2, 4, 8, 10, 14 measured lower)
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // six VALU
+  }
   wait_vm<phase_vm<MODE, S>()>();
   wide_barrier();
 }
