@@ -481,8 +481,11 @@ def q4k_extreme_blocks(n_blocks, seed):
     return b.reshape(-1)
 
 
+# the last three run whole rounds of 256 x 128 tiles and hand the columns of a half round to the
+# 128 x 128 kernel (M = 300: shifted-back row tiles in both parts)
 WIDE_CASES = [(256, 4096, 4096), (300, 512, 200), (520, 2048, 1000), (2048, 4096, 1024),
-              (2048, 4096, 4096), (256, 4096, 256)]
+              (2048, 4096, 4096), (256, 4096, 256), (512, 256, 24576), (300, 512, 24576),
+              (2048, 4096, 6144)]
 
 
 def gemm_split_count(M, N, K, tile_m):
@@ -498,7 +501,8 @@ def test_gemm_wide_tiles_equal_narrow(ctx, monkeypatch, M, K, N, act):
     w - 480, activation tiles by LDS DMA, last tiles shifted back inside the matrix); the
     128 x 128 kernel computes every element with the same integers and f32 steps, so the two
     agree bit for bit when both split K the same way (partial row and column tiles, 4 and 8
-    splits, none), and to f32 regrouping of the split sums otherwise; both modes."""
+    splits, none, a grid split between the two kernels), and to f32 regrouping of the split
+    sums otherwise; both modes."""
     w, x = gemm_case(ctx, M, K, N, seed=M + 7 * N + K, qtype=TYPE_Q4_K)
     wd, xd = ctx.to_device(w), ctx.to_device(x)
     monkeypatch.setenv("TPT_HIP_GEMM_TILE", "narrow")

@@ -1128,6 +1128,8 @@ bool gemm_wide(const GemmArgs& g) {
   return !(e && !strcmp(e, "narrow"));
 }
 
+constexpr int kRound = 256;  // workgroups the device runs at once (one per CU)
+
 // Splits of K for a grid of `tiles` output tiles that cannot fill the 256 CUs: the most that
 // still run in one round (tiles x splits <= 256), at least two super-blocks per split, at most 8.
 int splits_for(int tiles, int nkb) {
@@ -1166,6 +1168,35 @@ int launch_gemm_timed(const GemmArgs& g, hipStream_t s, hipEvent_t ev0, hipEvent
   const int tiles = ((g.N + BN - 1) / BN) * ((g.M + tm - 1) / tm);
   int ns = splits_for(tiles, g.K / 256);
   if (!g.part || g.part_floats < (size_t)ns * g.M * g.N) ns = 1;  // no workspace: one pass over K
+  if (wide && ns == 1) {
+    // Whole rounds of 256 x 128 tiles plus at most half a round more (M = 2048: N = 6144 or
+    // 14336): the columns of the last partial round go to the 128 x 128 kernel instead, one
+    // round of tiles with half the work each.  Both kernels give the same bits.
+    const int rows_w = (g.M + WBM - 1) / WBM, rows_n = (g.M + BM - 1) / BM, cols = (g.N + BN - 1) / BN;
+    const int full = tiles / kRound, rem = tiles % kRound;
+    if (full >= 1 && rem > 0 && rem <= kRound / 2 && (full * kRound) % rows_w == 0) {
+      const int cols_w = full * kRound / rows_w, cols_n = cols - cols_w;
+      if (cols_n >= 1 && cols_n * rows_n <= kRound) {
+        GemmArgs a = g, b = g;
+        a.N = cols_w * BN;
+        const size_t c0 = (size_t)cols_w * BN;
+        b.N = g.N - (int)c0;
+        b.w = g.w + c0 * g.w_stride;
+        b.y = g.y + c0;
+        if (g.resid) b.resid = g.resid + c0;
+        const dim3 ga((unsigned)cols_w, (unsigned)rows_w), gb((unsigned)cols_n, (unsigned)rows_n);
+        if (g.mode == GEMM_Q8K) {
+          hipExtLaunchKernelGGL((gemm_wide_kernel<GEMM_Q8K>), ga, dim3(GT), 0, s, ev0, nullptr, 0, a);
+          hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q4_K, GEMM_Q8K>), gb, dim3(GT), 0, s, nullptr, ev1, 0, b);
+        } else {
+          hipExtLaunchKernelGGL((gemm_wide_kernel<GEMM_F16>), ga, dim3(GT), 0, s, ev0, nullptr, 0, a);
+          hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q4_K, GEMM_F16>), gb, dim3(GT), 0, s, nullptr, ev1, 0, b);
+        }
+        TPT_HIP(hipGetLastError());
+        return TPT_OK;
+      }
+    }
+  }
   const dim3 grid((unsigned)((g.N + BN - 1) / BN), (unsigned)((g.M + tm - 1) / tm), (unsigned)ns);
   hipEvent_t e1 = ns > 1 ? nullptr : ev1;  // split-K: the stop event goes on the sum kernel
   if (wide) {
