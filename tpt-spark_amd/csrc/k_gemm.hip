@@ -1168,10 +1168,11 @@ int launch_gemm_timed(const GemmArgs& g, hipStream_t s, hipEvent_t ev0, hipEvent
   const int tiles = ((g.N + BN - 1) / BN) * ((g.M + tm - 1) / tm);
   int ns = splits_for(tiles, g.K / 256);
   if (!g.part || g.part_floats < (size_t)ns * g.M * g.N) ns = 1;  // no workspace: one pass over K
-  if (wide && ns == 1) {
+  if (wide && ns == 1 && g.mode == GEMM_Q8K) {
     // Whole rounds of 256 x 128 tiles plus at most half a round more (M = 2048: N = 6144 or
     // 14336): the columns of the last partial round go to the 128 x 128 kernel instead, one
-    // round of tiles with half the work each.  Both kernels give the same bits.
+    // round of tiles with half the work each.  Both kernels give the same bits.  (In f16 mode
+    // the half round of wide tiles is as fast.)
     const int rows_w = (g.M + WBM - 1) / WBM, rows_n = (g.M + BM - 1) / BM, cols = (g.N + BN - 1) / BN;
     const int full = tiles / kRound, rem = tiles % kRound;
     if (full >= 1 && rem > 0 && rem <= kRound / 2 && (full * kRound) % rows_w == 0) {
@@ -1185,13 +1186,8 @@ int launch_gemm_timed(const GemmArgs& g, hipStream_t s, hipEvent_t ev0, hipEvent
         b.y = g.y + c0;
         if (g.resid) b.resid = g.resid + c0;
         const dim3 ga((unsigned)cols_w, (unsigned)rows_w), gb((unsigned)cols_n, (unsigned)rows_n);
-        if (g.mode == GEMM_Q8K) {
-          hipExtLaunchKernelGGL((gemm_wide_kernel<GEMM_Q8K>), ga, dim3(GT), 0, s, ev0, nullptr, 0, a);
-          hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q4_K, GEMM_Q8K>), gb, dim3(GT), 0, s, nullptr, ev1, 0, b);
-        } else {
-          hipExtLaunchKernelGGL((gemm_wide_kernel<GEMM_F16>), ga, dim3(GT), 0, s, ev0, nullptr, 0, a);
-          hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q4_K, GEMM_F16>), gb, dim3(GT), 0, s, nullptr, ev1, 0, b);
-        }
+        hipExtLaunchKernelGGL((gemm_wide_kernel<GEMM_Q8K>), ga, dim3(GT), 0, s, ev0, nullptr, 0, a);
+        hipExtLaunchKernelGGL((gemm_kernel<TPT_TYPE_Q4_K, GEMM_Q8K>), gb, dim3(GT), 0, s, nullptr, ev1, 0, b);
         TPT_HIP(hipGetLastError());
         return TPT_OK;
       }
