@@ -37,7 +37,7 @@ constexpr int NCH_MAX = 256;   // chunks per kv head
 constexpr int MT = 32;         // output dims per merge workgroup
 constexpr int MSETS = ANT / MT;
 
-template <typename T, int HD, int G, int U>
+template <typename T, int HD, int G, int U, bool PIPE>
 __global__ void __launch_bounds__(ANT) attn_partial_kernel(const AttnArgs a, const float scale) {
   constexpr int LPP = KvTraits<T>::LPP;   // lanes per position
   constexpr int EPL = HD / LPP;           // elements per lane
@@ -78,21 +78,20 @@ __global__ void __launch_bounds__(ANT) attn_partial_kernel(const AttnArgs a, con
   const int n = p1 - p0;
   if (n <= 0) return;  // a chunk past the live length: the merge does not read its record
 
+  // Rounds of R*U positions.  PIPE: software-pipelined, the next round's rows requested before
+  // the current round's arithmetic (two register buffers, the first holding the preloaded
+  // round), so a long chunk pays its load latency about once per phase rather than once per
+  // round; otherwise each later round loads, then computes.  Same arithmetic in the same order.
+  auto load_rows = [&](const T* base_ptr, float (&buf)[U][EPL], int base) {
+#pragma unroll
+    for (int u = 0; u < U; u++) load_row<EPL>(base_ptr + (size_t)min(base + u * R + pg, plast) * HD, buf[u]);
+  };
+
   // phase 1: scores
   float mloc[G];
 #pragma unroll
   for (int h = 0; h < G; h++) mloc[h] = -INFINITY;
-  for (int base = p0; base < p1; base += R * U) {
-    float k[U][EPL];
-    if (base == p0) {
-#pragma unroll
-      for (int u = 0; u < U; u++)
-#pragma unroll
-        for (int e = 0; e < EPL; e++) k[u][e] = k0[u][e];
-    } else {
-#pragma unroll
-      for (int u = 0; u < U; u++) load_row<EPL>(K + (size_t)min(base + u * R + pg, plast) * HD, k[u]);
-    }
+  auto score_round = [&](const float (&k)[U][EPL], int base) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int p = base + u * R + pg;
@@ -107,6 +106,29 @@ __global__ void __launch_bounds__(ANT) attn_partial_kernel(const AttnArgs a, con
           if (li == 0) s_p[h][p - p0] = s;
         }
       }
+    }
+  };
+  if constexpr (PIPE) {
+    float k1[U][EPL];
+    for (int base = p0; base < p1; base += 2 * R * U) {
+      if (base + R * U < p1) load_rows(K, k1, base + R * U);
+      score_round(k0, base);
+      if (base + R * U >= p1) break;
+      if (base + 2 * R * U < p1) load_rows(K, k0, base + 2 * R * U);
+      score_round(k1, base + R * U);
+    }
+  } else {
+    for (int base = p0; base < p1; base += R * U) {
+      float k[U][EPL];
+      if (base == p0) {
+#pragma unroll
+        for (int u = 0; u < U; u++)
+#pragma unroll
+          for (int e = 0; e < EPL; e++) k[u][e] = k0[u][e];
+      } else {
+        load_rows(K, k, base);
+      }
+      score_round(k, base);
     }
   }
 #pragma unroll
@@ -150,20 +172,7 @@ __global__ void __launch_bounds__(ANT) attn_partial_kernel(const AttnArgs a, con
   for (int h = 0; h < G; h++)
 #pragma unroll
     for (int e = 0; e < EPL; e++) o[h][e] = 0.f;
-  for (int base = p0; base < p1; base += R * U) {
-    float vv[U][EPL];
-    if (base == p0) {
-#pragma unroll
-      for (int u = 0; u < U; u++)
-#pragma unroll
-        for (int e = 0; e < EPL; e++) vv[u][e] = vpre[u][e];
-    } else {
-#pragma unroll
-      for (int u = 0; u < U; u++) {
-        const int p = min(base + u * R + pg, plast);
-        load_row<EPL>(V + (size_t)p * HD, vv[u]);
-      }
-    }
+  auto pv_round = [&](const float (&vv)[U][EPL], int base) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int p = base + u * R + pg;
@@ -175,6 +184,29 @@ __global__ void __launch_bounds__(ANT) attn_partial_kernel(const AttnArgs a, con
           for (int e = 0; e < EPL; e++) o[h][e] = fmaf(w, vv[u][e], o[h][e]);
         }
       }
+    }
+  };
+  if constexpr (PIPE) {
+    float v1[U][EPL];
+    for (int base = p0; base < p1; base += 2 * R * U) {
+      if (base + R * U < p1) load_rows(V, v1, base + R * U);
+      pv_round(vpre, base);
+      if (base + R * U >= p1) break;
+      if (base + 2 * R * U < p1) load_rows(V, vpre, base + 2 * R * U);
+      pv_round(v1, base + R * U);
+    }
+  } else {
+    for (int base = p0; base < p1; base += R * U) {
+      float vv[U][EPL];
+      if (base == p0) {
+#pragma unroll
+        for (int u = 0; u < U; u++)
+#pragma unroll
+          for (int e = 0; e < EPL; e++) vv[u][e] = vpre[u][e];
+      } else {
+        load_rows(V, vv, base);
+      }
+      pv_round(vv, base);
     }
   }
 #pragma unroll
@@ -401,9 +433,17 @@ int launch_g(const AttnArgs& a, float scale, hipStream_t s) {
   if (a.chunk_len <= U1 * R)
     hipLaunchKernelGGL((attn_partial1_kernel<T, HD, G, U1>), grid, dim3(ANT), 0, s, a, scale);
   else if (a.chunk_len <= 4 * R)
-    hipLaunchKernelGGL((attn_partial_kernel<T, HD, G, 4>), grid, dim3(ANT), 0, s, a, scale);
-  else
-    hipLaunchKernelGGL((attn_partial_kernel<T, HD, G, 8>), grid, dim3(ANT), 0, s, a, scale);
+    hipLaunchKernelGGL((attn_partial_kernel<T, HD, G, 4, false>), grid, dim3(ANT), 0, s, a, scale);
+  else if constexpr (G == 1) {
+    // one query head per kv head (MHA): few registers per round, so the pipelined form pays;
+    // grids of more than two workgroups per CU take rounds of 4R (hd 96, 32 heads: 32768
+    // positions 84 -> 71 us with 4R, 16384 positions 41.6 -> 39.4 us with 8R)
+    if ((long)a.n_chunks * a.nkv * a.nqb > 512)
+      hipLaunchKernelGGL((attn_partial_kernel<T, HD, G, 4, true>), grid, dim3(ANT), 0, s, a, scale);
+    else
+      hipLaunchKernelGGL((attn_partial_kernel<T, HD, G, 8, true>), grid, dim3(ANT), 0, s, a, scale);
+  } else
+    hipLaunchKernelGGL((attn_partial_kernel<T, HD, G, 8, false>), grid, dim3(ANT), 0, s, a, scale);
   TPT_HIP(hipGetLastError());
   hipLaunchKernelGGL((attn_merge_kernel<HD, G>), dim3((unsigned)(a.nkv * G * HD / MT), (unsigned)a.nqb),
                      dim3(ANT), 0, s, (const float*)a.part, a.o, a.n_chunks, a.ldo, a.state, a.L_host,
