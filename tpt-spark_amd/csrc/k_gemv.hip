@@ -294,9 +294,12 @@ int dispatch_shape(const tpt_ctx* ctx, const GemvArgs& a, hipStream_t s, hipEven
   if constexpr (NMAT == 2) return by_bpp<WT, 2, 1, 2>(ctx, a, s, e0, e1, g);
   else if constexpr (WT == TPT_TYPE_F16) return by_bpp<WT, 1, 1, 2>(ctx, a, s, e0, e1, g);  // 128 B per group
   else {
-    // long rows: two rows per step (Q6_K and Q8_0 measured faster with one: 14336->4096
-    // 15.6 -> 14.9 us and 18.8 -> 18.3 us)
-    if (a.K > 8192 && WT != TPT_TYPE_Q6_K && WT != TPT_TYPE_Q8_0) return by_bpp<WT, 1, 2, 2>(ctx, a, s, e0, e1, g);
+    // Q6_K and Q8_0 (five and six loads per lane and step, against Q4_K's three): one step in
+    // flight per wave, one row per step (4096->14336: Q8_0 18.1 -> 14.3 us, Q6_K 12.2 -> 11.7 us;
+    // two steps or two rows per step were slower at every shape)
+    if constexpr (WT == TPT_TYPE_Q6_K || WT == TPT_TYPE_Q8_0) return by_bpp<WT, 1, 1, 1>(ctx, a, s, e0, e1, g);
+    // Q4_K and the rest: two steps in flight; long rows two rows per step
+    if (a.K > 8192) return by_bpp<WT, 1, 2, 2>(ctx, a, s, e0, e1, g);
     return by_bpp<WT, 1, 1, 2>(ctx, a, s, e0, e1, g);
   }
 }
