@@ -19,7 +19,9 @@
 //    position) and summed; then o = sum p v.  The record (o unnormalised, max, sum) goes to
 //    the partial buffer.  Chunks of up to 64 positions (the decode partition up to 4096
 //    positions with 8 kv heads) take attn_partial1: the chunk's K and V rows, scores and
-//    probabilities stay in registers, two workgroup barriers instead of four.
+//    probabilities stay in registers, two workgroup barriers instead of four.  With one query
+//    head per kv head the long chunks' rounds are software-pipelined (the next round's rows
+//    requested before the current round's arithmetic).
 //  * attn_merge, one workgroup per 32 output dims: combines the chunk records with the
 //    log-sum-exp rule; its first chunk loads are issued before the chunk weights are known.  The kernel boundary orders the two, so
 //    no device-wide fence or arrival counter is needed.
