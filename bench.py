@@ -272,8 +272,10 @@ def main():
     ap.add_argument("--prompt", type=int, default=PROMPT_LEN)
     ap.add_argument("--model", default="", help="existing GGUF (default: generate the 8B shape)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--leg", choices=["all", "gemv", "attn", "gemm", "causal", "decode"], default="all",
+    ap.add_argument("--leg", choices=["all", "gemv", "gemv-q6k-q80", "attn", "gemm", "causal", "decode"],
+                    default="all",
                     help="gemv: only the GEMV roofline leg and the copy calibration (profiling); "
+                         "gemv-q6k-q80: only the Q6_K and Q8_0 GEMV legs (profiling); "
                          "attn: only the decode-attention leg; gemm: only the prefill GEMM leg; "
                          "causal: only the prompt-attention leg; decode: only the end-to-end "
                          "prefill + decode run (profiling; no roofline or CPU legs)")
@@ -298,6 +300,11 @@ def main():
         return
     if args.leg == "causal":
         print(json.dumps({"prefill_attn": attn_causal_roofline(tp, ctx)}))
+        return
+    if args.leg == "gemv-q6k-q80":
+        print(json.dumps({"gemv_q6k": gemv_roofline(tp, ctx, iters=64, qtype=tp.TYPE_Q6_K),
+                          "gemv_q8_0": gemv_roofline(tp, ctx, iters=64, qtype=tp.TYPE_Q8_0),
+                          "copy": copy_calibration(ctx)}))
         return
     decode_only = args.leg == "decode"
     if not decode_only:
