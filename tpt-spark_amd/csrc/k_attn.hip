@@ -432,10 +432,9 @@ int launch_g(const AttnArgs& a, float scale, hipStream_t s) {
   const dim3 grid((unsigned)a.n_chunks, (unsigned)a.nkv, (unsigned)a.nqb);
   constexpr int R = ANT / KvTraits<T>::LPP;
   constexpr int U1 = 64 / R;  // one-pass form: chunks of up to 64 positions
+  static_assert(U1 * R >= 4 * R, "chunks of up to four rounds take the one-pass form");
   if (a.chunk_len <= U1 * R)
     hipLaunchKernelGGL((attn_partial1_kernel<T, HD, G, U1>), grid, dim3(ANT), 0, s, a, scale);
-  else if (a.chunk_len <= 4 * R)
-    hipLaunchKernelGGL((attn_partial_kernel<T, HD, G, 4, false>), grid, dim3(ANT), 0, s, a, scale);
   else if constexpr (G == 1) {
     // one query head per kv head (MHA): few registers per round, so the pipelined form pays;
     // grids of more than two workgroups per CU take rounds of 4R (hd 96, 32 heads: 32768
