@@ -644,8 +644,9 @@ __global__ void __launch_bounds__(GT, 1) gemm_kernel(const GemmArgs g) {
 // through a double-buffered tile of 128-byte rows.
 // GEMM_Q8K: one exact chain per super-block.  The tile holds w - 480 for w = sc * q in [0, 945],
 // so every partial sum is an integer of magnitude at most 256 * 128 * 480 < 2^24 (exact in f32),
-// and isum = chain + 480 * sum(q8) is formed by one f32 add: the rounding of the exact integer,
-// the value the two half chains of the 128 x 128 kernel give.  The rest of the block arithmetic is
+// and isum = chain + 480 * sum(q8) is formed by one more MFMA on the chain (two exact products,
+// one rounding): the rounding of the exact integer, the value the two half chains of the 128 x
+// 128 kernel give.  The rest of the block arithmetic is
 // that kernel's, so both produce the same bits.
 constexpr int WBM = 256, WBN = 128, WBK = 64;
 constexpr int WOFF = 480;  // a multiple of 32: 1024 sc + WOFF is exact in fp16 up to sc = 63
@@ -665,7 +666,8 @@ struct WideBlock {               // GEMM_Q8K: one super-block's per-row and per-
   _Float16 a16[WBM][LDG];        // activation per-16 sums
   _Float16 b16[WBN][LDG];        // weight mins, each repeated for its two 16-element halves
   float dx[WBM];                 // activation block scale
-  float sx[WBM];                 // 480 * the activation row's sum of q8 over the super-block
+  uint32_t sx[WBM];              // the activation row's sum of q8 over the super-block, S = 64 h + l
+                                 // (h, l of S's sign, |h| <= 512, |l| <= 63), as the fp16 pair (h, l)
   float dw[WBN], dm[WBN];        // weight d, dmin
 };
 // 158 KB: activation tiles by step mod 3 (the DMA runs two steps ahead), weight tiles by step
@@ -806,7 +808,9 @@ __device__ __forceinline__ void wide_store(const WideStage& st, _Float16* Bt, Wi
       const float fs = (float)s;               // |s| <= 128 * 128: exact
       const float tot = fs + dpp_mov<0xB1>(fs);  // + the other half of the row (lane ^ 1), exact
       B.dx[ra] = st.dx;
-      B.sx[ra] = (float)WOFF * tot;            // |.| <= 480 * 32768 < 2^24: exact
+      const int sum = (int)tot, h = sum / 64, l = sum - 64 * h;  // truncating: l has the sum's sign
+      const half2 hl = {(_Float16)h, (_Float16)l};
+      B.sx[ra] = __builtin_bit_cast(uint32_t, hl);
     }
   } else {
     const float d1 = d * (float)sc0, mm1 = dmin * (float)m0;
@@ -848,11 +852,31 @@ __device__ __forceinline__ void wide_mfma(const _Float16* A, const _Float16* Bt,
 
 // GEMM_Q8K end of a super-block, per element in f32 as the 128 x 128 kernel's block_end:
 // isum = chain + 480 sum(q8) (one rounding), y += d_x * fma(d_w, isum, -d_min * msum), the mins
-// term msum on the matrix cores (K = 16, exact).
-__device__ __forceinline__ void wide_block_end(const WideBlock& B, const floatx16 (&acc)[2][2], floatx16 (&out)[2][2]) {
+// term msum on the matrix cores (K = 16, exact).  The 480 sum(q8) term is added on the matrix
+// cores too: one MFMA with the chain as accumulator and two nonzero products per element,
+// 30720 h + 480 l = 480 (64 h + l) (exact, same sign as the sum), in place of an f32 add per
+// element.
+__device__ __forceinline__ void wide_block_end(const WideBlock& B, floatx16 (&acc)[2][2], floatx16 (&out)[2][2]) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int wm = wid >> 1, wn = wid & 1;
   const int lr = lane & 31, lk = 8 * (lane >> 5);
+  half8 bsx = {};  // B operand of the 480 sum(q8) MFMA: rows k = 0, 1 hold 64 * 480 and 480
+  if (lane < 32) {
+    bsx[0] = (_Float16)(64 * WOFF);
+    bsx[1] = (_Float16)WOFF;
+  }
+  // isum = chain + 480 sum(q8), in place, for the four tiles first
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    half8 asx = {};  // A operand: row 64 wm + 32 i + lr's pair (h, l) at k = 0, 1
+    if (lane < 32) {
+      const half2 hl = __builtin_bit_cast(half2, B.sx[64 * wm + 32 * i + lr]);
+      asx[0] = hl[0];
+      asx[1] = hl[1];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(asx, bsx, acc[i][j], 0, 0, 0);
+  }
   float dw[2], dm[2];
   half8 bm[2];
 #pragma unroll
@@ -866,14 +890,12 @@ __device__ __forceinline__ void wide_block_end(const WideBlock& B, const floatx1
   for (int i = 0; i < 2; i++) {
     const int r0 = 64 * wm + 32 * i;
     // the lane's 16 rows of tile i are 4 runs of 4 consecutive rows: one float4 each
-    float dxs[16], sxs[16];
+    float dxs[16];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
       const int r = r0 + q * 8 + (lane >> 5) * 4;
       const float4 v = *(const float4*)&B.dx[r];
-      const float4 u = *(const float4*)&B.sx[r];
       dxs[4 * q] = v.x; dxs[4 * q + 1] = v.y; dxs[4 * q + 2] = v.z; dxs[4 * q + 3] = v.w;
-      sxs[4 * q] = u.x; sxs[4 * q + 1] = u.y; sxs[4 * q + 2] = u.z; sxs[4 * q + 3] = u.w;
     }
     const half8 am = *(const half8*)&B.a16[r0 + lr][lk];
 #pragma unroll
@@ -881,8 +903,7 @@ __device__ __forceinline__ void wide_block_end(const WideBlock& B, const floatx1
       const floatx16 accm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm[j], floatx16{}, 0, 0, 0);
 #pragma unroll
       for (int e = 0; e < 16; e++) {
-        const float isum = acc[i][j][e] + sxs[e];
-        const float t = fmaf(dw[j], isum, -(dm[j] * accm[e]));
+        const float t = fmaf(dw[j], acc[i][j][e], -(dm[j] * accm[e]));
         out[i][j][e] = fmaf(dxs[e], t, out[i][j][e]);
       }
     }
