@@ -943,13 +943,14 @@ __device__ __forceinline__ void wide_phase(const GemmArgs& g, const WideOff& o, 
   wide_dma_a<(S + 2) % 4>(g, o, m0, kb2, s.a[ia2]);
   wide_load<MODE, (S + 2) % 4>(g, o, kb2, st);
   // the two waves of a SIMD reach the barrier together, so their MFMAs and their VALU work
-  // (the next tile's decode, the block end) cannot overlap each other; inside each wave, six
+  // (the next tile's decode, the block end) cannot overlap each other; inside each wave, seven
   // VALU instructions after every MFMA keep the VALU busy while the matrix core runs
-  // (q8k M=2048: +2-3% against the compiler's own order; 2, 4, 8, 10, 14 measured lower)
+  // (q8k M=2048: +2-3% against the compiler's own order with six; since the 480 sum(q8) term
+  // moved onto the matrix cores seven gain 2-3% more on gate|up and down; 4 and 5 measured lower)
 #pragma unroll
   for (int i = 0; i < 16; i++) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // six VALU
+    __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);  // seven VALU
   }
   wait_vm<phase_vm<MODE, S>()>();
   wide_barrier();
