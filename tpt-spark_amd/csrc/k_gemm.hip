@@ -946,7 +946,8 @@ __device__ __forceinline__ void wide_phase(const GemmArgs& g, const WideOff& o, 
   // (the next tile's decode, the block end) cannot overlap each other; inside each wave, seven
   // VALU instructions after every MFMA keep the VALU busy while the matrix core runs
   // (q8k M=2048: +2-3% against the compiler's own order with six; since the 480 sum(q8) term
-  // moved onto the matrix cores seven gain 2-3% more on gate|up and down; 4 and 5 measured lower)
+  // moved onto the matrix cores seven gain 2-3% more on gate|up and down; 4, 5, 8, 9 measured
+  // lower)
 #pragma unroll
   for (int i = 0; i < 16; i++) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
